@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""bf16 GEMM throughput on one MI355X through libt0g's C ABI.
+
+One step = one C = A*B GEMM (bf16 in, fp32 accumulate, bf16 out, row-major NN)
+at BASELINE configs[1], M = N = K = 4096, inputs N(0,1)*0.02 resident in HBM.
+Prints ONE JSON line.  Besides `value` (TFLOPS of the timed steps) the line
+carries the dominant kernel's roofline (HIP events on the stream the kernels
+run on), the other BASELINE configs under "extra", and the CPU oracle timed on
+this host under "cpu_baseline".
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "t0-gpu_amd"))
+
+METRIC = "bf16 GEMM TFLOPS at 4096³ and 8192³ on 1 MI355X; % of dense bf16 MFMA peak"
+PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+PEAK_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(torch, m, n, k, layout, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    a_shape = (m, k) if layout in ("NT", "NN") else (k, m)
+    b_shape = (n, k) if layout in ("NT", "TT") else (k, n)
+    a = (torch.randn(a_shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    b = (torch.randn(b_shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    return a, b
+
+
+def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None):
+    a, b = make_inputs(torch, m, n, k, layout, seed)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16)
+    kname = t0g.gemm_kernel_name(desc)
+    for _ in range(warmup):
+        rt.gemm_desc(desc)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        rt.gemm_desc(desc)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t_start
+    ev_ms = e0.elapsed_time(e1)
+    res = {"kernel": kname, "wall_ms_per_step": wall_s * 1e3 / steps, "event_ms_per_launch": ev_ms / steps,
+           "flop": 2.0 * m * n * k, "bytes_min": 2.0 * (m * k + k * n) + 2.0 * m * n}
+    if out is not None:
+        out["tensors"] = (a, b, c)
+    return res
+
+
+def mlp_step(t0g, torch, rt, stream, steps, warmup):
+    """forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
+    dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out."""
+    bsz, d_in, d_hid = 1024, 4096, 11008
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((bsz, d_in), generator=g, device="cuda").to(torch.bfloat16)
+    w1 = ((torch.rand((d_in, d_hid), generator=g, device="cuda") - 1.0) * (2.0 / d_in) ** 0.5).to(torch.bfloat16)
+    w2 = ((torch.rand((d_hid, d_in), generator=g, device="cuda") - 1.0) * (2.0 / d_hid) ** 0.5).to(torch.bfloat16)
+    dy = (torch.randn((bsz, d_in), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    h = torch.empty((bsz, d_hid), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((bsz, d_in), dtype=torch.bfloat16, device="cuda")
+    dh = torch.empty_like(h)
+    dx = torch.empty_like(x)
+    dw1 = torch.empty_like(w1)
+    dw2 = torch.empty_like(w2)
+    p = lambda t: t.data_ptr()
+    descs = [
+        t0g.gemm_desc(p(x), p(w1), p(h), bsz, d_hid, d_in, transpose="NN", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(h), p(w2), p(y), bsz, d_in, d_hid, transpose="NN", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(dy), p(w2), p(dh), bsz, d_hid, d_in, transpose="NT", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(dh), p(w1), p(dx), bsz, d_in, d_hid, transpose="NT", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(h), p(dy), p(dw2), d_hid, d_in, bsz, transpose="TN", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(x), p(dh), p(dw1), d_in, d_hid, bsz, transpose="TN", out_dtype=t0g.BF16),
+    ]
+    for _ in range(warmup):
+        for d in descs:
+            rt.gemm_desc(d)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        for d in descs:
+            rt.gemm_desc(d)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flop = 6 * 2.0 * bsz * d_in * d_hid
+    return {"ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+            "frac_of_peak": flop / (ms * 1e-3) / 1e12 / PEAK_TFLOPS,
+            "kernels": [t0g.gemm_kernel_name(d) for d in descs]}
+
+
+def cpu_baseline(torch, tensors, m, n, k, min_seconds):
+    """The CPU oracle (oracle/ref_gemm.c, a bit-exact restatement of the reference's
+    CPU GEMM) on this host: the whole 4096^3 product, repeated to ~min_seconds."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    a, b, _ = tensors
+    a_np = a.cpu().view(torch.int16).numpy().view(np.uint16)
+    b_np = b.cpu().view(torch.int16).numpy().view(np.uint16)
+    threads = oracle.num_threads()
+    reps, t_total = 0, 0.0
+    while t_total < min_seconds and reps < 20:
+        t0 = time.perf_counter()
+        oracle.gemm("NN", a_np, b_np, m, n, k, threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    fast = 2.0 * m * n * k * reps / t_total / 1e12
+    rows = 16
+    t0 = time.perf_counter()
+    oracle.gemm_nt_naive(a_np, np.ascontiguousarray(b_np.T), m, k, n, rows=(0, rows))
+    t_naive = time.perf_counter() - t0
+    naive = 2.0 * rows * n * k / t_naive / 1e12
+    return {"value": fast, "unit": "TFLOPS", "cores": threads, "kind": "port",
+            "sample": f"full {m}x{n}x{k} NN product x{reps} ({t_total:.1f} s, vectorised + OpenMP, "
+                      f"bit-identical to the reference loop)",
+            "naive_single_thread": {"value": naive, "unit": "TFLOPS", "cores": 1,
+                                    "sample": f"{rows} output rows of {m}x{n}x{k}, reference loop order"}}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build measures the GEMM on one GPU only "
+              f"(no multi-GPU path); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import t0g
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    rt = t0g.GpuRuntime.new(0)
+    stream = torch.cuda.Stream()
+    rt.set_stream(stream.cuda_stream)
+    torch.cuda.set_stream(stream)
+
+    M = N = K = 4096
+    keep = {}
+    log(f"[bench] 4096^3 NN bf16: warmup {args.warmup}, steps {args.steps}")
+    main_res = time_gemm(t0g, torch, rt, stream, M, N, K, "NN", args.steps, args.warmup, out=keep)
+    tflops = main_res["flop"] / (main_res["wall_ms_per_step"] * 1e-3) / 1e12
+    kern_tflops = main_res["flop"] / (main_res["event_ms_per_launch"] * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get(main_res["kernel"])
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["wall_ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: A, B ~ N(0,1)*0.02 from seed (torch.randn on device), bf16",
+        "config": {"workload": "gemm_bf16_nn_4096x4096x4096_bf16out", "M": M, "N": N, "K": K,
+                   "layout": "NN (C = A*B, row-major)", "accumulate": "fp32", "out": "bf16",
+                   "kernel": main_res["kernel"], "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kern_tflops / PEAK_TFLOPS, 4), "traffic": traffic,
+                     "per_launch_flop": main_res["flop"], "avg_launch_ms": round(main_res["event_ms_per_launch"], 5)},
+    }
+
+    if not args.no_extra:
+        extra = {}
+        steps8 = max(5, args.steps // 2)
+        log(f"[bench] 8192^3 NN bf16: steps {steps8}")
+        r8 = time_gemm(t0g, torch, rt, stream, 8192, 8192, 8192, "NN", steps8, 3, seed=4)
+        t8 = r8["flop"] / (r8["event_ms_per_launch"] * 1e-3) / 1e12
+        extra["gemm_nn_8192^3"] = {"tflops": round(t8, 2), "frac_of_peak": round(t8 / PEAK_TFLOPS, 4),
+                                   "ms_per_launch": round(r8["event_ms_per_launch"], 4), "kernel": r8["kernel"]}
+        for name, (m, n, k) in {"thin_128x4096x4096": (128, 4096, 4096),
+                                "splitk_256x256xK32768": (256, 256, 32768)}.items():
+            log(f"[bench] {name}")
+            r = time_gemm(t0g, torch, rt, stream, m, n, k, "NT", args.steps, args.warmup, seed=9)
+            sec = r["event_ms_per_launch"] * 1e-3
+            extra[name] = {"tflops": round(r["flop"] / sec / 1e12, 2),
+                           "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1),
+                           "frac_of_hbm": round(r["bytes_min"] / sec / 1e9 / PEAK_GBS, 4),
+                           "us_per_gemm": round(sec * 1e6, 2), "kernel": r["kernel"]}
+        log("[bench] MLP step")
+        extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5), 2)
+        line["extra"] = extra
+
+    if args.cpu_seconds > 0:
+        log("[bench] CPU baseline (oracle on host cores)")
+        line["cpu_baseline"] = cpu_baseline(torch, keep["tensors"], M, N, K, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    rt.set_stream(None)
+    rt.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,242 @@
+/*
+ * t0g.h -- C ABI of the MI355X (gfx950) bf16 GEMM path for the T0-GPU call surface.
+ *
+ * Drop-in boundary for the reference's GEMM hot path.  The reference is Rust
+ * (GeisYaO/t0-gpu); each entry point below names the Rust item it replaces
+ * (paths relative to the reference root).  Plain pointers, sizes and device
+ * addresses only (uint64_t, like the reference's GpuBuffer::gpu_addr()).
+ *
+ * Errors: every fallible call returns a t0g_status (0 = OK) and leaves a
+ * thread-local message in t0g_last_error().  The reference returns
+ * Result<_, String> and panics on invalid GemmConfigs (src/t0/gemm_gen.rs:256-266,
+ * src/t0/tile_ir.rs:630-655); here invalid configs return
+ * T0G_ERR_UNSUPPORTED_CONFIG instead.  A device that saw a kernel/HIP failure or
+ * a wait timeout is poisoned and refuses further work, as GpuRuntime does
+ * (src/ignis/gpu_context.rs:150-157, 270-287).
+ *
+ * Threading: a t0g_device is safe to share between threads; its calls are
+ * serialised by an internal mutex and run on one HIP stream (the reference
+ * uses one in-order AQL queue, src/kfd/mod.rs:1290-1348).
+ */
+#ifndef T0G_H
+#define T0G_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T0G_API __attribute__((visibility("default")))
+
+typedef enum t0g_status {
+    T0G_OK = 0,
+    T0G_ERR_INVALID_ARG = 1,
+    T0G_ERR_UNSUPPORTED_CONFIG = 2,
+    T0G_ERR_HIP = 3,
+    T0G_ERR_TIMEOUT = 4,
+    T0G_ERR_POISONED = 5,
+    T0G_ERR_NO_DEVICE = 6,
+    T0G_ERR_OUT_OF_MEMORY = 7
+} t0g_status;
+
+/* GemmTranspose (src/t0/gemm_gen.rs:24-29) / TileTranspose (src/t0/tile_ir.rs:73-78),
+ * extended with the layouts the reference builds by host transposes
+ * (src/t0/gemm_gen.rs:482-542, src/ignis/ops/bf16_matmul.rs:215-308).
+ * Operand storage, all row-major bf16:
+ *   NT: A [M][lda>=K], B [N][ldb>=K]   C = A * B^T   (reference default: Y = X * WT^T)
+ *   NN: A [M][lda>=K], B [K][ldb>=N]   C = A * B
+ *   TN: A [K][lda>=M], B [K][ldb>=N]   C = A^T * B
+ *   TT: A [K][lda>=M], B [N][ldb>=K]   C = A^T * B^T                              */
+typedef enum t0g_transpose { T0G_NT = 0, T0G_NN = 1, T0G_TN = 2, T0G_TT = 3 } t0g_transpose;
+
+/* EpilogueOp of gemm_gen (src/t0/gemm_gen.rs:41-49). */
+typedef enum t0g_epilogue {
+    T0G_EPI_STORE_F32 = 0,
+    T0G_EPI_BIAS_ADD = 1,
+    T0G_EPI_BIAS_ADD_RELU = 2
+} t0g_epilogue;
+
+typedef enum t0g_dtype { T0G_F32 = 0, T0G_BF16 = 1 } t0g_dtype;
+
+/* GemmConfig (src/t0/gemm_gen.rs:56-84).  Same fields and meaning; the valid
+ * tile set is the MI355X one (t0g_config_preset).  split_k: 0 = None. */
+typedef struct t0g_gemm_config {
+    uint32_t tile_m;
+    uint32_t tile_n;
+    uint32_t tile_k;
+    uint32_t wg_size;       /* threads per workgroup (wave64: 64 * waves) */
+    uint32_t split_k;       /* Option<u32>: 0 or 1 = no split */
+    uint32_t lds_pad;       /* accepted for layout compatibility; the gfx950 kernels swizzle instead */
+    uint32_t n_col_passes;  /* must be 1 on gfx950 (one pass covers tile_n) */
+    uint8_t use_lds;
+    uint8_t double_buffer;
+    uint8_t swap_grid;      /* true: grid x -> N tiles, y -> M tiles (src/t0/gemm_gen.rs:286-296) */
+    uint8_t wgp_mode;       /* RDNA3 only; ignored on CDNA4 */
+    uint32_t transpose;     /* t0g_transpose */
+    uint32_t epilogue;      /* t0g_epilogue */
+} t0g_gemm_config;
+
+typedef struct t0g_device t0g_device;
+typedef struct t0g_kernel t0g_kernel;
+
+/* ---- library ------------------------------------------------------------ */
+T0G_API const char *t0g_last_error(void);
+T0G_API const char *t0g_version(void);
+
+/* ---- configuration and selection (host only, no GPU needed) ------------ */
+
+/* GemmConfig::tile_* presets (src/t0/gemm_gen.rs:88-145), MI355X tile set:
+ * "tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64". */
+T0G_API int t0g_config_preset(const char *name, t0g_gemm_config *out);
+/* generate()'s feasibility check (src/t0/gemm_gen.rs:253-266, is_feasible 194-197). */
+T0G_API int t0g_config_validate(const t0g_gemm_config *cfg);
+/* GemmConfig::n_waves (src/t0/gemm_gen.rs:152): wg_size / 64 on wave64. */
+T0G_API uint32_t t0g_config_n_waves(const t0g_gemm_config *cfg);
+/* GemmConfig::lds_total (src/t0/gemm_gen.rs:162-170). */
+T0G_API uint32_t t0g_config_lds_total(const t0g_gemm_config *cfg);
+/* GemmConfig::name (src/t0/gemm_gen.rs:207-227), same tag scheme. */
+T0G_API int t0g_config_name(const t0g_gemm_config *cfg, char *buf, size_t len);
+
+/* auto_select(m, k, n) -> GemmConfig (src/t0/gemm_gen.rs:320-322): table
+ * re-derived for 256 CUs (NT layout, f32 store epilogue). */
+T0G_API int t0g_auto_select(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
+/* tile_auto_select(m, k, n, transpose) (src/t0/tile_ir.rs:471-568). */
+T0G_API int t0g_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose,
+                                 t0g_gemm_config *out);
+
+/* compute_grid (src/t0/gemm_gen.rs:286-296): grid in THREADS, x = tiles * wg_size. */
+T0G_API int t0g_compute_grid(const t0g_gemm_config *cfg, uint32_t m, uint32_t n,
+                             uint32_t *grid_x, uint32_t *grid_y);
+/* compute_grid_split_k (src/t0/gemm_gen.rs:298-309); split_k must be a power of two. */
+T0G_API int t0g_compute_grid_split_k(const t0g_gemm_config *cfg, uint32_t m, uint32_t n,
+                                     uint32_t split_k, uint32_t *grid_x, uint32_t *grid_y);
+/* compute_grid_auto (src/t0/gemm_gen.rs:402-409). */
+T0G_API int t0g_compute_grid_auto(const t0g_gemm_config *cfg, uint32_t m, uint32_t n,
+                                  uint32_t *grid_x, uint32_t *grid_y);
+/* tile_ir::compute_grid (src/t0/tile_ir.rs:3193-3202): [x, y, 1] in threads. */
+T0G_API int t0g_tile_compute_grid(const t0g_gemm_config *cfg, uint32_t m, uint32_t n,
+                                  uint32_t grid[3]);
+
+/* build_kernargs (src/t0/gemm_gen.rs:414-430): 40 bytes
+ * [X u64 @0, WT u64 @8, Y u64 @16, K u32 @24, N u32 @28, split_k_shift u32 @32 (=0),
+ *  y_split_stride u32 @36 (= M*N*4 when split_k > 1, else 0)].  Note the
+ * reference's argument order (k, n, m). */
+T0G_API int t0g_build_kernargs(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                               uint32_t m, const t0g_gemm_config *cfg, uint8_t out[40]);
+/* build_kernargs_with_bias (src/t0/gemm_gen.rs:438-456): 48 bytes, bias u64 @40. */
+T0G_API int t0g_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t k,
+                                         uint32_t n, uint32_t m, const t0g_gemm_config *cfg,
+                                         uint64_t bias, uint8_t out[48]);
+/* tile_ir::build_kernargs_m (src/t0/tile_ir.rs:3173-3190): 44 bytes, M u32 @40,
+ * split_k_shift = log2(split_k), y_split_stride = 0 (the reference value). */
+T0G_API int t0g_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                                 uint32_t m, const t0g_gemm_config *cfg, uint8_t out[44]);
+
+/* Backward helpers (src/t0/gemm_gen.rs:482-542), same argument meaning:
+ * forward Y[M,N] = X[M,K] * WT[N,K]^T. */
+T0G_API int t0g_auto_select_backward_data(uint32_t m, uint32_t n_orig, uint32_t k_orig,
+                                          t0g_gemm_config *out);
+T0G_API int t0g_auto_select_backward_weight(uint32_t m, uint32_t n_orig, uint32_t k_orig,
+                                            t0g_gemm_config *out);
+T0G_API int t0g_build_kernargs_backward_data(uint64_t dy, uint64_t w, uint64_t dx, uint32_t m,
+                                             uint32_t n_orig, uint32_t k_orig,
+                                             const t0g_gemm_config *cfg, uint8_t out[40]);
+T0G_API int t0g_build_kernargs_backward_weight(uint64_t dy_t, uint64_t x_t, uint64_t dw,
+                                               uint32_t m, uint32_t n_orig, uint32_t k_orig,
+                                               const t0g_gemm_config *cfg, uint8_t out[40]);
+T0G_API int t0g_compute_grid_backward_data(const t0g_gemm_config *cfg, uint32_t m,
+                                           uint32_t k_orig, uint32_t *grid_x, uint32_t *grid_y);
+T0G_API int t0g_compute_grid_backward_weight(const t0g_gemm_config *cfg, uint32_t n_orig,
+                                             uint32_t k_orig, uint32_t *grid_x, uint32_t *grid_y);
+
+/* ---- device runtime (HIP) ------------------------------------------------ */
+
+T0G_API int t0g_device_count(int *count);
+/* KfdDevice::open + GpuRuntime::new (src/kfd/mod.rs:257-453, src/ignis/gpu_context.rs:86-147):
+ * selects the HIP device, creates its stream, loads the gfx950 code object. */
+T0G_API int t0g_device_open(int ordinal, t0g_device **out);
+T0G_API int t0g_device_close(t0g_device *dev);
+/* Run subsequent work on a caller-owned hipStream_t (NULL: back to the device's own). */
+T0G_API int t0g_device_set_stream(t0g_device *dev, void *hip_stream);
+T0G_API int t0g_device_get_stream(t0g_device *dev, void **hip_stream);
+T0G_API int t0g_device_is_poisoned(t0g_device *dev, int *poisoned);
+
+/* KfdDevice::alloc_vram / GpuRuntime::{alloc, alloc_zero} (src/kfd/mod.rs:572,
+ * src/ignis/gpu_context.rs:437-454).  Returns the device address. */
+T0G_API int t0g_alloc(t0g_device *dev, size_t bytes, uint64_t *addr);
+T0G_API int t0g_alloc_zero(t0g_device *dev, size_t bytes, uint64_t *addr);
+/* GpuBuffer drop (src/kfd/mod.rs:1057-1081); waits for the stream first. */
+T0G_API int t0g_free(t0g_device *dev, uint64_t addr);
+/* GpuBuffer::{write, read, zero} (src/kfd/mod.rs:1000-1055): synchronous. */
+T0G_API int t0g_memcpy_h2d(t0g_device *dev, uint64_t dst, const void *src, size_t bytes);
+T0G_API int t0g_memcpy_d2h(t0g_device *dev, void *dst, uint64_t src, size_t bytes);
+T0G_API int t0g_memset(t0g_device *dev, uint64_t dst, int value, size_t bytes);
+
+/* generate(&cfg) + compile + GpuKernel::load, cached by name as
+ * GpuRuntime::ensure_kernel_t0 does (src/t0/gemm_gen.rs:253-281,
+ * src/ignis/gpu_context.rs:171-218).  Selects the precompiled gfx950 kernel
+ * for cfg; it takes the 40-byte (48 with a bias epilogue) gemm_gen kernargs. */
+T0G_API int t0g_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out);
+/* tile_ir::lower_gemm twin (src/t0/tile_ir.rs:585): 44-byte kernargs with M @40
+ * (+ bias u64 @44 with a bias epilogue, src/compile.rs:93-111 ordering). */
+T0G_API int t0g_tile_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out);
+/* GpuKernel::load(&device, &elf, &KernelLoadConfig{workgroup_size, lds_size})
+ * (src/kfd/mod.rs:2559-2651, 2655): any gfx950 code object, launched raw. */
+T0G_API int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size,
+                            const char *symbol, const uint32_t workgroup_size[3],
+                            uint32_t lds_size, t0g_kernel **out);
+/* CompiledKernel fields (src/t0/dsl.rs:8-21). */
+T0G_API int t0g_kernel_info(const t0g_kernel *kernel, uint32_t *wg_size, uint32_t *lds_size,
+                            uint32_t *kernarg_size, char *name, size_t name_len);
+
+/* GpuRuntime::dispatch (src/ignis/gpu_context.rs:264-288): grid in THREADS,
+ * kernargs as bytes; synchronous.  _async returns after enqueueing
+ * (gpu_context.rs:332-342); t0g_wait_idle waits for all of them (gpu_context.rs:382). */
+T0G_API int t0g_dispatch(t0g_device *dev, const t0g_kernel *kernel, const uint32_t grid_threads[3],
+                         const void *kernargs, size_t kernargs_len);
+T0G_API int t0g_dispatch_async(t0g_device *dev, const t0g_kernel *kernel,
+                               const uint32_t grid_threads[3], const void *kernargs,
+                               size_t kernargs_len);
+T0G_API int t0g_wait_idle(t0g_device *dev);
+
+/* ---- one-shot typed GEMM (no reference counterpart; replaces the
+ *      select/kernargs/grid/dispatch/host-reduce sequence the reference's
+ *      callers write out, e.g. examples/test_gemm_correctness.rs:150-215) ---- */
+typedef struct t0g_gemm_desc {
+    uint64_t a, b, c;               /* device addresses: bf16 A, bf16 B, f32|bf16 C */
+    uint64_t bias;                  /* f32[N] for the bias epilogues, else 0 */
+    uint64_t workspace;             /* fp32 split-K workspace, 0 = library-managed */
+    uint64_t workspace_bytes;
+    uint32_t m, n, k;
+    uint32_t lda, ldb, ldc;         /* elements; 0 = packed */
+    uint32_t transpose;             /* t0g_transpose */
+    uint32_t out_dtype;             /* t0g_dtype */
+    uint32_t epilogue;              /* t0g_epilogue */
+    uint32_t split_k;               /* 0 = from config / auto_select, 1 = none, >1 forced */
+    const t0g_gemm_config *config;  /* NULL = t0g_auto_select(m, k, n) */
+} t0g_gemm_desc;
+
+/* Enqueue C = op(A) * op(B) (+ epilogue) on the device stream (asynchronous).
+ * split_k > 1: fp32 partial planes, then a deterministic plane-ordered reduce. */
+T0G_API int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *desc);
+/* Bytes of workspace t0g_gemm would use for desc (0 without split-K). */
+T0G_API int t0g_gemm_workspace_size(const t0g_gemm_desc *desc, size_t *bytes);
+/* Name of the gfx950 kernel symbol t0g_gemm would launch for desc. */
+T0G_API int t0g_gemm_kernel_name(const t0g_gemm_desc *desc, char *buf, size_t len);
+
+/* ---- test hooks ------------------------------------------------------------ */
+/* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
+ * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
+ * real device fault. */
+T0G_API int t0g_debug_fail_hip_call(int n);
+/* Wait timeout of t0g_wait_idle / t0g_dispatch in milliseconds (default 60000);
+ * the reference polls for 5 s (src/kfd/mod.rs:1607-1642). */
+T0G_API int t0g_set_wait_timeout_ms(uint32_t ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* T0G_H */

@@ -1,0 +1,189 @@
+"""numpy front end of the CPU oracle (oracle/ref_gemm.c) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this module, and only as the checker (or as the timed CPU baseline); the
+product path never imports it.  See ref_gemm.c for the reference lines each
+function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+if not os.path.exists(LIB_PATH):
+    build()
+
+_lib = ctypes.CDLL(LIB_PATH)
+_sz = ctypes.c_size_t
+_p = ctypes.c_void_p
+
+
+def _sig(name, restype, *argtypes):
+    f = getattr(_lib, name)
+    f.restype = restype
+    f.argtypes = list(argtypes)
+    return f
+
+
+_sig("oracle_f32_to_bf16_rne", ctypes.c_uint16, ctypes.c_float)
+_sig("oracle_f32_to_bf16_trunc", ctypes.c_uint16, ctypes.c_float)
+_sig("oracle_bf16_to_f32", ctypes.c_float, ctypes.c_uint16)
+_sig("oracle_f32_to_bf16_rne_array", None, _p, _p, _sz)
+_sig("oracle_bf16_to_f32_array", None, _p, _p, _sz)
+_sig("oracle_rand_bf16_xorshift", None, _p, _sz, ctypes.c_uint64)
+_sig("oracle_rand_bf16_lcg", None, _p, _sz, ctypes.c_uint64)
+_sig("oracle_make_bf16_suite", None, _p, _sz, ctypes.c_uint64)
+_sig("oracle_linear_init_f32", None, _p, _sz, _sz, ctypes.c_uint64)
+_sig("oracle_randn_bf16", None, _p, _sz, ctypes.c_uint64, ctypes.c_double)
+_sig("oracle_gemm_nt_naive", None, _p, _p, _p, _sz, _sz, _sz)
+_sig("oracle_gemm_nt_naive_rows", None, _p, _p, _p, _sz, _sz, _sz, _sz, _sz)
+_sig("oracle_gemm", None, ctypes.c_int, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _sz, ctypes.c_int)
+_sig("oracle_gemm_krange", None, ctypes.c_int, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _sz, _sz, ctypes.c_int)
+_sig("oracle_splitk_reduce", None, _p, _p, _sz, _sz)
+_sig("oracle_transpose_bf16", None, _p, _p, _sz, _sz)
+_sig("oracle_num_threads", ctypes.c_int)
+
+LAYOUT = {"NT": 0, "NN": 1, "TN": 2, "TT": 3}
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    assert a.dtype == np.uint16, a.dtype
+    return a
+
+
+def f32_to_bf16_rne(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    _lib.oracle_f32_to_bf16_rne_array(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def f32_to_bf16_trunc(x):
+    return (np.ascontiguousarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(x):
+    x = _u16(x)
+    out = np.empty(x.shape, dtype=np.float32)
+    _lib.oracle_bf16_to_f32_array(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def rand_bf16_xorshift(n, seed):
+    out = np.empty(n, dtype=np.uint16)
+    _lib.oracle_rand_bf16_xorshift(out.ctypes.data, n, seed)
+    return out
+
+
+def rand_bf16_lcg(n, seed):
+    out = np.empty(n, dtype=np.uint16)
+    _lib.oracle_rand_bf16_lcg(out.ctypes.data, n, seed)
+    return out
+
+
+def make_bf16_suite(n, seed):
+    out = np.empty(n, dtype=np.uint16)
+    _lib.oracle_make_bf16_suite(out.ctypes.data, n, seed)
+    return out
+
+
+def linear_init_f32(in_features, out_features, seed=42):
+    out = np.empty((in_features, out_features), dtype=np.float32)
+    _lib.oracle_linear_init_f32(out.ctypes.data, in_features, out_features, seed)
+    return out
+
+
+def randn_bf16(n, seed, sigma=1.0):
+    out = np.empty(n, dtype=np.uint16)
+    _lib.oracle_randn_bf16(out.ctypes.data, n, seed, sigma)
+    return out
+
+
+def gemm_nt_naive(x, wt, m, k, n, rows=None):
+    """Faithful single-thread reference loop; rows=(begin, end) computes a row block only."""
+    x, wt = _u16(x), _u16(wt)
+    y = np.zeros((m, n), dtype=np.float32)
+    if rows is None:
+        _lib.oracle_gemm_nt_naive(x.ctypes.data, wt.ctypes.data, y.ctypes.data, m, k, n)
+    else:
+        _lib.oracle_gemm_nt_naive_rows(x.ctypes.data, wt.ctypes.data, y.ctypes.data, m, k, n, rows[0], rows[1])
+    return y
+
+
+def gemm(layout, a, b, m, n, k, lda=None, ldb=None, threads=0):
+    """Bit-identical fast restatement, any of NT/NN/TN/TT (see ref_gemm.c)."""
+    lay = LAYOUT[layout] if isinstance(layout, str) else layout
+    a, b = _u16(a), _u16(b)
+    a_mk = lay in (0, 1)
+    b_kn = lay in (1, 2)
+    lda = lda or (k if a_mk else m)
+    ldb = ldb or (n if b_kn else k)
+    c = np.empty((m, n), dtype=np.float32)
+    _lib.oracle_gemm(lay, a.ctypes.data, b.ctypes.data, c.ctypes.data, m, n, k, lda, ldb, n, threads)
+    return c
+
+
+def gemm_rows(layout, a, b, m, n, k, rows, threads=0):
+    """Rows `rows` (an index array) of the product, with the same per-element order."""
+    lay = LAYOUT[layout] if isinstance(layout, str) else layout
+    a = _u16(a).reshape(-1)
+    rows = np.asarray(rows)
+    if lay in (0, 1):   # A stored [M][K]: take the rows
+        a_sub = a.reshape(m, k)[rows]
+        return gemm(lay, a_sub, b, len(rows), n, k, threads=threads)
+    a_sub = np.ascontiguousarray(a.reshape(k, m)[:, rows])   # A stored [K][M]: take the columns
+    return gemm(lay, a_sub, b, len(rows), n, k, threads=threads)
+
+
+def gemm_krange(layout, a, b, m, n, k, k_begin, k_end, threads=0):
+    lay = LAYOUT[layout] if isinstance(layout, str) else layout
+    a, b = _u16(a), _u16(b)
+    a_mk = lay in (0, 1)
+    b_kn = lay in (1, 2)
+    lda = k if a_mk else m
+    ldb = n if b_kn else k
+    c = np.empty((m, n), dtype=np.float32)
+    _lib.oracle_gemm_krange(lay, a.ctypes.data, b.ctypes.data, c.ctypes.data, m, n, lda, ldb, n, k_begin, k_end,
+                            threads)
+    return c
+
+
+def splitk_reduce(planes):
+    planes = np.ascontiguousarray(planes, dtype=np.float32)
+    sk = planes.shape[0]
+    y = np.empty(planes.shape[1:], dtype=np.float32)
+    _lib.oracle_splitk_reduce(planes.ctypes.data, y.ctypes.data, y.size, sk)
+    return y
+
+
+def transpose_bf16(a, rows, cols):
+    a = _u16(a)
+    out = np.empty(rows * cols, dtype=np.uint16)
+    _lib.oracle_transpose_bf16(a.ctypes.data, out.ctypes.data, rows, cols)
+    return out.reshape(cols, rows)
+
+
+def num_threads():
+    return _lib.oracle_num_threads()
+
+
+def parity(c_gpu, c_ref, k):
+    """The north-star gate: relF <= 5e-3 and max|d| <= 1e-2 * sqrt(K/256).  Returns (ok, relF, maxabs, bound)."""
+    c_gpu = np.asarray(c_gpu, dtype=np.float64)
+    c_ref = np.asarray(c_ref, dtype=np.float64)
+    diff = c_gpu - c_ref
+    nref = np.linalg.norm(c_ref)
+    relf = float(np.linalg.norm(diff) / nref) if nref > 0 else float(np.linalg.norm(diff))
+    maxabs = float(np.max(np.abs(diff))) if diff.size else 0.0
+    bound = 1e-2 * np.sqrt(max(k, 1) / 256.0)
+    return (relf <= 5e-3 and maxabs <= bound), relf, maxabs, bound

@@ -1,0 +1,305 @@
+// Host-only half of the C ABI: GemmConfig presets, validation, naming,
+// auto_select for 256 CUs, grids, kernarg builders and the backward helpers.
+// No HIP calls here, so every function in this file works without a GPU.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "t0g.h"
+#include "t0g_internal.h"
+
+namespace t0g {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return T0G_OK;
+}
+
+// MI355X tile set.  Every entry has a precompiled kernel family in
+// t0g_gemm_gfx950.hsaco (gemm_gfx950.hip).  `eff` is the sustained fraction of
+// the per-CU MFMA rate the tile reaches when the CU is full, `wg_per_cu` how
+// many of its workgroups fit one CU (LDS 2*(BM+BN)*128 B, registers).
+const TileDef kTiles[kNumTiles] = {
+    {256, 256, 256, 0.80, 1, "t0g_gemm_256x256_k64"},
+    {128, 128, 256, 0.60, 2, "t0g_gemm_128x128_k64"},
+    {64, 64, 256, 0.30, 2, "t0g_gemm_64x64_k64"},
+};
+
+const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size) {
+    if (tile_k != kTileK) return nullptr;
+    for (const TileDef &t : kTiles)
+        if (t.bm == tile_m && t.bn == tile_n && t.wg == wg_size) return &t;
+    return nullptr;
+}
+
+void make_config(const TileDef &t, uint32_t split_k, t0g_gemm_config *out) {
+    memset(out, 0, sizeof *out);
+    out->tile_m = t.bm;
+    out->tile_n = t.bn;
+    out->tile_k = kTileK;
+    out->wg_size = t.wg;
+    out->split_k = split_k > 1 ? split_k : 0;
+    out->lds_pad = 0;
+    out->n_col_passes = 1;
+    out->use_lds = 1;
+    out->double_buffer = 1;
+    out->swap_grid = 1;
+    out->wgp_mode = 0;
+    out->transpose = T0G_NT;
+    out->epilogue = T0G_EPI_STORE_F32;
+}
+
+uint32_t cfg_split(const t0g_gemm_config *cfg) { return cfg->split_k > 1 ? cfg->split_k : 1; }
+
+int validate(const t0g_gemm_config *cfg) {
+    if (!cfg) return fail(T0G_ERR_INVALID_ARG, "config is NULL");
+    if (!find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size))
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG,
+                    "no gfx950 kernel for tile %ux%u k%u wg%u (supported: 256x256/128x128/64x64, k64, wg256)",
+                    cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
+    if (!cfg->use_lds || !cfg->double_buffer)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "gfx950 kernels always use double-buffered LDS");
+    if (cfg->n_col_passes != 1)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "n_col_passes must be 1 on gfx950 (got %u)", cfg->n_col_passes);
+    if (cfg->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", cfg->transpose);
+    if (cfg->epilogue > T0G_EPI_BIAS_ADD_RELU) return fail(T0G_ERR_INVALID_ARG, "bad epilogue %u", cfg->epilogue);
+    const uint32_t sk = cfg_split(cfg);
+    if (sk > kMaxSplitK || (sk & (sk - 1)) != 0)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u must be a power of two <= %u", sk, kMaxSplitK);
+    return ok();
+}
+
+// ---- selection model ---------------------------------------------------------
+// Modelled time of one (tile, split) choice on MI355X: 256 CUs, 2.5 PF dense
+// bf16, 8 TB/s HBM.  Each CU holds up to wg_per_cu workgroups that share its
+// MFMA rate; the busiest CU's share of the work sets the compute time.  Memory
+// time counts compulsory operand and output bytes plus split-K workspace
+// traffic; a split-K reduce costs an extra launch.
+double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk) {
+    const double tiles = (double)((m + t.bm - 1) / t.bm) * (double)((n + t.bn - 1) / t.bn);
+    const uint32_t kc = ((k + sk - 1) / sk + kTileK - 1) / kTileK * kTileK;
+    const double wgs = tiles * sk;
+    const double per_cu = ceil(wgs / kNumCUs);   // workgroups on the busiest CU
+    const double cu_rate = kPeakFlops / kNumCUs * t.eff;
+    const double t_comp = per_cu * (2.0 * t.bm * t.bn * (double)(kc > 0 ? kc : kTileK)) / cu_rate;
+    double bytes = 2.0 * ((double)m * k + (double)k * n) + 4.0 * (double)m * n;
+    if (sk > 1) bytes += 8.0 * (double)m * n * sk;
+    const double t_mem = bytes / kPeakBytes;
+    double t_us = (t_comp > t_mem ? t_comp : t_mem) * 1e6;
+    if (sk > 1) t_us += 2.0;   // second launch
+    return t_us;
+}
+
+void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
+    const TileDef *best = &kTiles[0];
+    uint32_t best_sk = 1;
+    double best_t = 1e300;
+    for (const TileDef &t : kTiles) {
+        for (uint32_t sk = 1; sk <= kMaxSplitK; sk *= 2) {
+            if (sk > 1 && k < sk * 4 * kTileK) break;   // keep >= 4 K tiles per split
+            const double tt = model_time_us(t, m, k, n, sk);
+            if (tt < best_t * 0.98) {   // prefer earlier (bigger tile, fewer splits) on near ties
+                best_t = tt;
+                best = &t;
+                best_sk = sk;
+            }
+        }
+    }
+    make_config(*best, best_sk, out);
+}
+
+}  // namespace t0g
+
+using namespace t0g;
+
+extern "C" {
+
+const char *t0g_last_error(void) { return g_last_error.c_str(); }
+const char *t0g_version(void) { return "t0g 0.1.0 (gfx950)"; }
+
+int t0g_config_preset(const char *name, t0g_gemm_config *out) {
+    if (!name || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    for (const TileDef &t : kTiles) {
+        char buf[64];
+        snprintf(buf, sizeof buf, "tile_%ux%u_k%u", t.bm, t.bn, kTileK);
+        if (strcmp(buf, name) == 0) {
+            make_config(t, 0, out);
+            return ok();
+        }
+    }
+    return fail(T0G_ERR_UNSUPPORTED_CONFIG, "unknown preset '%s'", name);
+}
+
+int t0g_config_validate(const t0g_gemm_config *cfg) { return validate(cfg); }
+
+uint32_t t0g_config_n_waves(const t0g_gemm_config *cfg) { return cfg ? cfg->wg_size / kWaveSize : 0; }
+
+uint32_t t0g_config_lds_total(const t0g_gemm_config *cfg) {
+    if (!cfg) return 0;
+    const uint32_t per_buffer = (cfg->tile_m + cfg->tile_n) * cfg->tile_k * 2;
+    return cfg->double_buffer ? 2 * per_buffer : per_buffer;
+}
+
+int t0g_config_name(const t0g_gemm_config *cfg, char *buf, size_t len) {
+    if (!cfg || !buf || len == 0) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::string s = "t0_gemm_" + std::to_string(cfg->tile_m) + "x" + std::to_string(cfg->tile_n) + "_k" +
+                    std::to_string(cfg->tile_k);
+    s += cfg->use_lds ? (cfg->double_buffer ? "_ldsdb" : "_lds") : "_direct";
+    if (cfg->split_k > 1) s += "_sk" + std::to_string(cfg->split_k);
+    if (cfg->n_col_passes > 1) s += "_" + std::to_string(cfg->n_col_passes) + "p";
+    if (!cfg->swap_grid) s += "_mg";
+    if (cfg->wgp_mode) s += "_wgp";
+    static const char *tr[] = {"", "_nn", "_tn", "_tt"};
+    if (cfg->transpose <= T0G_TT) s += tr[cfg->transpose];
+    if (cfg->epilogue == T0G_EPI_BIAS_ADD) s += "_bias";
+    if (cfg->epilogue == T0G_EPI_BIAS_ADD_RELU) s += "_bias_relu";
+    if (s.size() + 1 > len) return fail(T0G_ERR_INVALID_ARG, "name buffer too small (%zu < %zu)", len, s.size() + 1);
+    memcpy(buf, s.c_str(), s.size() + 1);
+    return ok();
+}
+
+int t0g_auto_select(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
+    if (!out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (m == 0 || n == 0) return fail(T0G_ERR_INVALID_ARG, "auto_select: m=%u n=%u must be > 0", m, n);
+    select_config(m, k, n, out);
+    return ok();
+}
+
+int t0g_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose, t0g_gemm_config *out) {
+    if (transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", transpose);
+    int rc = t0g_auto_select(m, k, n, out);
+    if (rc == T0G_OK) out->transpose = transpose;
+    return rc;
+}
+
+static int grid_common(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t sk, uint32_t *gx, uint32_t *gy) {
+    if (!cfg || !gx || !gy) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (cfg->tile_m == 0 || cfg->tile_n == 0) return fail(T0G_ERR_INVALID_ARG, "zero tile size");
+    const uint32_t eff_n = cfg->tile_n * (cfg->n_col_passes ? cfg->n_col_passes : 1);
+    const uint32_t tm = (m + cfg->tile_m - 1) / cfg->tile_m;
+    const uint32_t tn = (n + eff_n - 1) / eff_n;
+    if (cfg->swap_grid) {
+        *gx = tn * cfg->wg_size;
+        *gy = tm * sk;
+    } else {
+        *gx = tm * cfg->wg_size;
+        *gy = tn * sk;
+    }
+    return ok();
+}
+
+int t0g_compute_grid(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t *gx, uint32_t *gy) {
+    return grid_common(cfg, m, n, 1, gx, gy);
+}
+
+int t0g_compute_grid_split_k(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t split_k, uint32_t *gx,
+                             uint32_t *gy) {
+    if (split_k == 0 || (split_k & (split_k - 1)) != 0)
+        return fail(T0G_ERR_INVALID_ARG, "split_k=%u must be power of 2", split_k);
+    return grid_common(cfg, m, n, split_k, gx, gy);
+}
+
+int t0g_compute_grid_auto(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t *gx, uint32_t *gy) {
+    if (!cfg) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    const uint32_t sk = cfg_split(cfg);
+    return sk > 1 ? t0g_compute_grid_split_k(cfg, m, n, sk, gx, gy) : t0g_compute_grid(cfg, m, n, gx, gy);
+}
+
+int t0g_tile_compute_grid(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t grid[3]) {
+    if (!grid) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    int rc = grid_common(cfg, m, n, cfg ? cfg_split(cfg) : 1, &grid[0], &grid[1]);
+    grid[2] = 1;
+    return rc;
+}
+
+static void put_u64(uint8_t *p, uint64_t v) { memcpy(p, &v, 8); }   // x86-64 and gfx950 are little-endian
+static void put_u32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+
+int t0g_build_kernargs(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                       const t0g_gemm_config *cfg, uint8_t out[40]) {
+    if (!cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    const uint32_t sk = cfg_split(cfg);
+    const uint32_t y_stride = sk > 1 ? m * n * 4 : 0;
+    put_u64(out + 0, x);
+    put_u64(out + 8, wt);
+    put_u64(out + 16, y);
+    put_u32(out + 24, k);
+    put_u32(out + 28, n);
+    put_u32(out + 32, 0);
+    put_u32(out + 36, y_stride);
+    return ok();
+}
+
+int t0g_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                                 const t0g_gemm_config *cfg, uint64_t bias, uint8_t out[48]) {
+    int rc = t0g_build_kernargs(x, wt, y, k, n, m, cfg, out);
+    if (rc == T0G_OK) put_u64(out + 40, bias);
+    return rc;
+}
+
+int t0g_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                         const t0g_gemm_config *cfg, uint8_t out[44]) {
+    if (!cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    uint32_t shift = 0;
+    switch (cfg_split(cfg)) {
+        case 2: shift = 1; break;
+        case 4: shift = 2; break;
+        case 8: shift = 3; break;
+        case 16: shift = 4; break;
+        default: shift = 0; break;
+    }
+    put_u64(out + 0, x);
+    put_u64(out + 8, wt);
+    put_u64(out + 16, y);
+    put_u32(out + 24, k);
+    put_u32(out + 28, n);
+    put_u32(out + 32, shift);
+    put_u32(out + 36, 0);
+    put_u32(out + 40, m);
+    return ok();
+}
+
+int t0g_auto_select_backward_data(uint32_t m, uint32_t n_orig, uint32_t k_orig, t0g_gemm_config *out) {
+    return t0g_auto_select(m, n_orig, k_orig, out);
+}
+
+int t0g_auto_select_backward_weight(uint32_t m, uint32_t n_orig, uint32_t k_orig, t0g_gemm_config *out) {
+    return t0g_auto_select(n_orig, m, k_orig, out);
+}
+
+int t0g_build_kernargs_backward_data(uint64_t dy, uint64_t w, uint64_t dx, uint32_t m, uint32_t n_orig,
+                                     uint32_t k_orig, const t0g_gemm_config *cfg, uint8_t out[40]) {
+    return t0g_build_kernargs(dy, w, dx, n_orig, k_orig, m, cfg, out);
+}
+
+int t0g_build_kernargs_backward_weight(uint64_t dy_t, uint64_t x_t, uint64_t dw, uint32_t m, uint32_t n_orig,
+                                       uint32_t k_orig, const t0g_gemm_config *cfg, uint8_t out[40]) {
+    return t0g_build_kernargs(dy_t, x_t, dw, m, k_orig, n_orig, cfg, out);
+}
+
+int t0g_compute_grid_backward_data(const t0g_gemm_config *cfg, uint32_t m, uint32_t k_orig, uint32_t *gx,
+                                   uint32_t *gy) {
+    return t0g_compute_grid_auto(cfg, m, k_orig, gx, gy);
+}
+
+int t0g_compute_grid_backward_weight(const t0g_gemm_config *cfg, uint32_t n_orig, uint32_t k_orig, uint32_t *gx,
+                                     uint32_t *gy) {
+    return t0g_compute_grid_auto(cfg, n_orig, k_orig, gx, gy);
+}
+
+}  // extern "C"

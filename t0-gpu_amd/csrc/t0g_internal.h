@@ -1,0 +1,42 @@
+// Internal declarations shared by the host-side translation units of libt0g.
+#ifndef T0G_INTERNAL_H
+#define T0G_INTERNAL_H
+
+#include <stdint.h>
+
+#include <string>
+
+#include "t0g.h"
+
+namespace t0g {
+
+constexpr uint32_t kTileK = 64;
+constexpr uint32_t kWaveSize = 64;
+constexpr uint32_t kNumCUs = 256;
+constexpr uint32_t kMaxSplitK = 64;
+constexpr double kPeakFlops = 2.5e15;   // dense bf16 MFMA, MI355X
+constexpr double kPeakBytes = 8.0e12;   // HBM3E, MI355X
+
+struct TileDef {
+    uint32_t bm, bn, wg;
+    double eff;
+    uint32_t wg_per_cu;
+    const char *symbol_prefix;
+};
+constexpr int kNumTiles = 3;
+extern const TileDef kTiles[kNumTiles];
+
+extern thread_local std::string g_last_error;
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int ok();
+
+const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size);
+void make_config(const TileDef &t, uint32_t split_k, t0g_gemm_config *out);
+uint32_t cfg_split(const t0g_gemm_config *cfg);
+int validate(const t0g_gemm_config *cfg);
+void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
+double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);
+
+}  // namespace t0g
+
+#endif

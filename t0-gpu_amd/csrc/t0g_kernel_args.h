@@ -1,0 +1,40 @@
+/* Kernel-argument block shared by the host runtime and the gfx950 kernels.
+ * Every GEMM kernel in t0g_gemm_gfx950.hsaco takes exactly one T0gGemmArgs by
+ * value; the host fills it and passes its bytes through hipModuleLaunchKernel's
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER, the HIP analogue of the reference writing a
+ * kernarg blob into its AQL kernarg ring (src/kfd/mod.rs:2902). */
+#ifndef T0G_KERNEL_ARGS_H
+#define T0G_KERNEL_ARGS_H
+#include <stdint.h>
+
+typedef struct T0gGemmArgs {
+    uint64_t a;              /* op(A) operand base address (bf16)                 */
+    uint64_t b;              /* op(B) operand base address (bf16)                 */
+    uint64_t c;              /* output base address (f32 or bf16)                 */
+    uint64_t bias;           /* f32[N] bias for the bias epilogues, else 0        */
+    uint64_t c_split_stride; /* bytes between split-K output planes               */
+    uint32_t m, n, k;        /* problem size                                      */
+    uint32_t lda, ldb, ldc;  /* leading dimensions in elements                    */
+    uint32_t k_per_split;    /* K elements per split slice (multiple of tile_k)   */
+    uint32_t tiles_m;        /* output tiles along M covered by the grid          */
+    uint32_t tiles_n;        /* output tiles along N covered by the grid          */
+    uint32_t epilogue;       /* 0 store, 1 +bias[col], 2 +bias[col] then ReLU     */
+    uint32_t group_m;        /* tile-order group height (L2 reuse), >= 1          */
+    uint32_t flags;          /* bit0: remap block ids across the 8 XCDs           */
+} T0gGemmArgs;
+
+typedef struct T0gReduceArgs {
+    uint64_t ws;             /* f32 planes [splits][m][ldw]                       */
+    uint64_t c;              /* output (f32 or bf16) [m][ldc]                     */
+    uint64_t bias;           /* f32[N] or 0                                       */
+    uint64_t plane_elems;    /* elements between planes                           */
+    uint32_t m, n, ldw, ldc;
+    uint32_t splits;
+    uint32_t epilogue;
+    uint32_t grid_blocks;    /* launched workgroups (256 threads each)           */
+    uint32_t pad_;
+} T0gReduceArgs;
+
+#define T0G_FLAG_XCD_REMAP 1u
+
+#endif

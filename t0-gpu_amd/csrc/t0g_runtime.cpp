@@ -1,0 +1,756 @@
+// Device half of the C ABI: HIP device/stream/memory, the embedded gfx950
+// code object, the reference-layout dispatch path and the typed GEMM entry.
+//
+// The reference talks to /dev/kfd directly: VRAM allocation, an AQL queue
+// with a doorbell, an ELF loader that patches RSRC1 (src/kfd/mod.rs).  Here
+// those become hipMalloc, one HIP stream per device handle and
+// hipModuleLoadData / hipModuleLaunchKernel on a code object built ahead of
+// time by hipcc for gfx950.
+#include <hip/hip_runtime_api.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+
+#include <atomic>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "t0g.h"
+#include "t0g_internal.h"
+#include "t0g_kernel_args.h"
+
+// The gfx950 code object, embedded at build time (T0G_HSACO_FILE is set by the Makefile).
+__asm__(".section .rodata.t0g_hsaco,\"a\",@progbits\n"
+        ".p2align 12\n"
+        ".hidden t0g_hsaco_begin\n"
+        ".globl t0g_hsaco_begin\n"
+        "t0g_hsaco_begin:\n"
+        ".incbin \"" T0G_HSACO_FILE "\"\n"
+        ".hidden t0g_hsaco_end\n"
+        ".globl t0g_hsaco_end\n"
+        "t0g_hsaco_end:\n"
+        ".byte 0\n"
+        ".previous\n");
+extern "C" const unsigned char t0g_hsaco_begin[];
+extern "C" const unsigned char t0g_hsaco_end[];
+
+namespace t0g {
+
+enum class KernelKind { GemmGen, TileGemm, Raw };
+
+}  // namespace t0g
+
+struct t0g_kernel {
+    t0g::KernelKind kind;
+    t0g_gemm_config cfg;          // GemmGen / TileGemm
+    hipFunction_t fn = nullptr;   // Raw
+    uint32_t wg[3] = {1, 1, 1};
+    uint32_t lds = 0;
+    uint32_t kernarg_size = 0;
+    std::string name;
+};
+
+struct t0g_device {
+    int ordinal = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    std::mutex mu;
+    bool poisoned = false;
+    std::string poison_reason;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    std::vector<std::unique_ptr<t0g_kernel>> kernels;
+    std::unordered_map<std::string, t0g_kernel *> kernel_cache;
+    std::vector<hipModule_t> extra_modules;
+    std::set<uint64_t> allocations;
+    uint64_t ws = 0;
+    size_t ws_bytes = 0;
+};
+
+namespace t0g {
+
+static std::atomic<int> g_fail_countdown{0};
+static std::atomic<uint32_t> g_wait_timeout_ms{60000};
+
+// Every HIP call goes through here so a test can make the n-th one fail.
+static bool injected_failure() {
+    int c = g_fail_countdown.load();
+    while (c > 0) {
+        if (g_fail_countdown.compare_exchange_weak(c, c - 1)) return c == 1;
+    }
+    return false;
+}
+
+#define T0G_HIP(expr) (::t0g::injected_failure() ? hipErrorLaunchFailure : (expr))
+
+static int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? T0G_ERR_OUT_OF_MEMORY : T0G_ERR_HIP, "%s failed: %s (%d)", what,
+                hipGetErrorString(e), (int)e);
+}
+
+// A failure of work already sent to the device poisons the handle, as the
+// reference's GpuRuntime does after a dispatch timeout.
+static int poison(t0g_device *dev, int code) {
+    dev->poisoned = true;
+    dev->poison_reason = g_last_error;
+    return code;
+}
+
+static int check_usable(t0g_device *dev) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    if (dev->poisoned)
+        return fail(T0G_ERR_POISONED, "device poisoned by an earlier failure: %s", dev->poison_reason.c_str());
+    hipError_t e = T0G_HIP(hipSetDevice(dev->ordinal));
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return T0G_OK;
+}
+
+static double now_ms() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
+}
+
+// Wait for the stream with a time limit (the reference polls the AQL read
+// pointer for 5 s, src/kfd/mod.rs:1607-1642).  Timeout poisons the device.
+static int wait_stream(t0g_device *dev) {
+    const double t0 = now_ms();
+    const uint32_t limit = g_wait_timeout_ms.load();
+    for (;;) {
+        hipError_t e = T0G_HIP(hipStreamQuery(dev->stream));
+        if (e == hipSuccess) return T0G_OK;
+        if (e != hipErrorNotReady) return poison(dev, hip_fail(e, "hipStreamQuery"));
+        if (now_ms() - t0 > limit)
+            return poison(dev, fail(T0G_ERR_TIMEOUT, "GPU wait timed out after %u ms", limit));
+        timespec ts = {0, 20000};
+        nanosleep(&ts, nullptr);
+    }
+}
+
+static int get_function(t0g_device *dev, const std::string &name, hipFunction_t *out) {
+    auto it = dev->fns.find(name);
+    if (it != dev->fns.end()) {
+        *out = it->second;
+        return T0G_OK;
+    }
+    hipFunction_t f = nullptr;
+    hipError_t e = T0G_HIP(hipModuleGetFunction(&f, dev->module, name.c_str()));
+    if (e != hipSuccess) return hip_fail(e, ("hipModuleGetFunction(" + name + ")").c_str());
+    dev->fns.emplace(name, f);
+    *out = f;
+    return T0G_OK;
+}
+
+static int launch(t0g_device *dev, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
+                  void *args, size_t args_size) {
+    void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
+                     HIP_LAUNCH_PARAM_END};
+    hipError_t e = T0G_HIP(hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, 0, dev->stream, nullptr, extra));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipModuleLaunchKernel"));
+    return T0G_OK;
+}
+
+static const char *layout_tag(uint32_t t) {
+    static const char *tags[] = {"nt", "nn", "tn", "tt"};
+    return tags[t & 3];
+}
+
+static bool a_k_major(uint32_t t) { return t == T0G_NT || t == T0G_NN; }
+static bool b_k_major(uint32_t t) { return t == T0G_NT || t == T0G_TT; }
+
+// A fully resolved GEMM launch (both the typed API and the reference-layout
+// dispatch path end here).
+struct GemmPlan {
+    const TileDef *tile;
+    uint32_t transpose;
+    bool out_bf16;
+    bool aligned;
+    uint32_t splits;
+    uint32_t k_per_split;
+    uint32_t tiles_m, tiles_n;
+    std::string symbol;
+};
+
+static bool operands_aligned(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
+                             uint32_t t) {
+    if ((a & 15) || (b & 15) || (lda & 7) || (ldb & 7)) return false;
+    if (a_k_major(t) ? (k & 7) != 0 : ((m & 7) != 0 || m < 8)) return false;
+    if (b_k_major(t) ? (k & 7) != 0 : ((n & 7) != 0 || n < 8)) return false;
+    return true;
+}
+
+static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, bool aligned, uint32_t m, uint32_t n,
+                     uint32_t k, uint32_t split_req, GemmPlan *p) {
+    if (!aligned && tile->bm == 256) tile = &kTiles[1];   // no element-wise-load variant of the 256x256 tile
+    p->tile = tile;
+    p->transpose = transpose;
+    p->out_bf16 = out_bf16;
+    p->aligned = aligned;
+    p->tiles_m = (m + tile->bm - 1) / tile->bm;
+    p->tiles_n = (n + tile->bn - 1) / tile->bn;
+    uint32_t sk = split_req ? split_req : 1;
+    uint32_t kps = k;
+    if (sk > 1) {
+        kps = ((k + sk - 1) / sk + kTileK - 1) / kTileK * kTileK;
+        sk = (k + kps - 1) / kps;
+        if (sk <= 1) {
+            sk = 1;
+            kps = k;
+        }
+    }
+    if (kps == 0) kps = kTileK;   // K == 0: one empty slice, C = 0 (+ epilogue)
+    p->splits = sk;
+    p->k_per_split = kps;
+    const bool partial = sk > 1;
+    p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
+                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? "" : "_u");
+    if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
+        return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
+    return T0G_OK;
+}
+
+// Per-thread operand offsets inside the kernels are 32-bit element counts.
+static int check_extent(const char *what, uint64_t rows, uint64_t ld) {
+    if (rows * ld >= (1ull << 31))
+        return fail(T0G_ERR_INVALID_ARG, "%s spans %llu elements; the gfx950 kernels address < 2^31", what,
+                    (unsigned long long)(rows * ld));
+    return T0G_OK;
+}
+
+static int ensure_workspace(t0g_device *dev, size_t bytes) {
+    if (dev->ws_bytes >= bytes) return T0G_OK;
+    if (dev->ws) {
+        hipError_t e = T0G_HIP(hipFree((void *)dev->ws));   // hipFree waits for work using it
+        dev->ws = 0;
+        dev->ws_bytes = 0;
+        if (e != hipSuccess) return poison(dev, hip_fail(e, "hipFree(workspace)"));
+    }
+    void *p = nullptr;
+    hipError_t e = T0G_HIP(hipMalloc(&p, bytes));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+    dev->ws = (uint64_t)p;
+    dev->ws_bytes = bytes;
+    return T0G_OK;
+}
+
+struct GemmOperands {
+    uint64_t a, b, c, bias;
+    uint32_t m, n, k, lda, ldb, ldc;
+    uint32_t epilogue;
+    uint64_t c_split_stride;   // reference-layout path: caller-owned planes
+};
+
+// Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
+// the partial planes go to `ws` and the reduce kernel produces C.
+static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws) {
+    hipFunction_t f = nullptr;
+    int rc = get_function(dev, p.symbol, &f);
+    if (rc) return rc;
+    T0gGemmArgs args;
+    memset(&args, 0, sizeof args);
+    args.a = o.a;
+    args.b = o.b;
+    args.m = o.m;
+    args.n = o.n;
+    args.k = o.k;
+    args.lda = o.lda;
+    args.ldb = o.ldb;
+    args.k_per_split = p.k_per_split;
+    args.tiles_m = p.tiles_m;
+    args.tiles_n = p.tiles_n;
+    args.group_m = 8;
+    args.flags = T0G_FLAG_XCD_REMAP;
+    const bool reduce = p.splits > 1 && o.c_split_stride == 0;
+    if (reduce) {
+        args.c = ws;
+        args.ldc = o.n;
+        args.c_split_stride = (uint64_t)o.m * o.n * 4;
+        args.epilogue = T0G_EPI_STORE_F32;
+    } else {
+        args.c = o.c;
+        args.ldc = o.ldc;
+        args.c_split_stride = o.c_split_stride;
+        args.epilogue = o.epilogue;
+        args.bias = o.bias;
+    }
+    rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.tile->wg, &args, sizeof args);
+    if (rc || !reduce) return rc;
+
+    hipFunction_t fr = nullptr;
+    rc = get_function(dev, p.out_bf16 ? "t0g_splitk_reduce_bf16" : "t0g_splitk_reduce_f32", &fr);
+    if (rc) return rc;
+    T0gReduceArgs r;
+    memset(&r, 0, sizeof r);
+    r.ws = ws;
+    r.c = o.c;
+    r.bias = o.bias;
+    r.plane_elems = (uint64_t)o.m * o.n;
+    r.m = o.m;
+    r.n = o.n;
+    r.ldw = o.n;
+    r.ldc = o.ldc;
+    r.splits = p.splits;
+    r.epilogue = o.epilogue;
+    const uint64_t total = (uint64_t)o.m * o.n;
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    r.grid_blocks = (uint32_t)blocks;
+    return launch(dev, fr, (uint32_t)blocks, 1, 1, 256, &r, sizeof r);
+}
+
+static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *plan, GemmOperands *o) {
+    if (!d) return fail(T0G_ERR_INVALID_ARG, "desc is NULL");
+    if (d->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", d->transpose);
+    if (d->out_dtype > T0G_BF16) return fail(T0G_ERR_INVALID_ARG, "bad out_dtype %u", d->out_dtype);
+    if (d->epilogue > T0G_EPI_BIAS_ADD_RELU) return fail(T0G_ERR_INVALID_ARG, "bad epilogue %u", d->epilogue);
+    if (d->epilogue != T0G_EPI_STORE_F32 && !d->bias)
+        return fail(T0G_ERR_INVALID_ARG, "bias epilogue without a bias pointer");
+    const uint32_t t = d->transpose;
+    o->a = d->a;
+    o->b = d->b;
+    o->c = d->c;
+    o->bias = d->bias;
+    o->m = d->m;
+    o->n = d->n;
+    o->k = d->k;
+    o->lda = d->lda ? d->lda : (a_k_major(t) ? d->k : d->m);
+    o->ldb = d->ldb ? d->ldb : (b_k_major(t) ? d->k : d->n);
+    o->ldc = d->ldc ? d->ldc : d->n;
+    o->epilogue = d->epilogue;
+    o->c_split_stride = 0;
+    if (o->ldc < o->n) return fail(T0G_ERR_INVALID_ARG, "ldc=%u < n=%u", o->ldc, o->n);
+    if (a_k_major(t) ? o->lda < o->k : o->lda < o->m) return fail(T0G_ERR_INVALID_ARG, "lda=%u too small", o->lda);
+    if (b_k_major(t) ? o->ldb < o->k : o->ldb < o->n) return fail(T0G_ERR_INVALID_ARG, "ldb=%u too small", o->ldb);
+    int rc;
+    if (d->config) {
+        *cfg = *d->config;
+    } else {
+        select_config(d->m ? d->m : 1, d->k, d->n ? d->n : 1, cfg);
+    }
+    cfg->transpose = t;
+    cfg->epilogue = d->epilogue;
+    if ((rc = validate(cfg))) return rc;
+    if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
+    if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
+    const uint32_t sk = d->split_k ? d->split_k : cfg_split(cfg);
+    if (sk > kMaxSplitK) return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u > %u", sk, kMaxSplitK);
+    const TileDef *tile = find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
+    const bool aligned = operands_aligned(d->a, d->b, d->m, d->n, d->k, o->lda, o->ldb, t);
+    return make_plan(tile, t, d->out_dtype == T0G_BF16, aligned, d->m, d->n, d->k, sk, plan);
+}
+
+}  // namespace t0g
+
+using namespace t0g;
+
+extern "C" {
+
+int t0g_debug_fail_hip_call(int n) {
+    if (n < 0) return fail(T0G_ERR_INVALID_ARG, "n must be >= 0");
+    g_fail_countdown.store(n);
+    return ok();
+}
+
+int t0g_set_wait_timeout_ms(uint32_t ms) {
+    if (ms == 0) return fail(T0G_ERR_INVALID_ARG, "timeout must be > 0");
+    g_wait_timeout_ms.store(ms);
+    return ok();
+}
+
+int t0g_device_count(int *count) {
+    if (!count) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    int n = 0;
+    hipError_t e = T0G_HIP(hipGetDeviceCount(&n));
+    if (e == hipErrorNoDevice || (e == hipSuccess && n == 0)) {
+        *count = 0;
+        return ok();
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    *count = n;
+    return ok();
+}
+
+int t0g_device_open(int ordinal, t0g_device **out) {
+    if (!out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = T0G_HIP(hipGetDeviceCount(&n));
+    if (e == hipErrorNoDevice || (e == hipSuccess && n == 0)) return fail(T0G_ERR_NO_DEVICE, "no HIP device");
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (ordinal < 0 || ordinal >= n) return fail(T0G_ERR_INVALID_ARG, "device %d out of range [0,%d)", ordinal, n);
+    if ((e = T0G_HIP(hipSetDevice(ordinal))) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    if ((e = T0G_HIP(hipGetDeviceProperties(&prop, ordinal))) != hipSuccess)
+        return hip_fail(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(T0G_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", ordinal,
+                    prop.gcnArchName);
+    std::unique_ptr<t0g_device> dev(new t0g_device);
+    dev->ordinal = ordinal;
+    if ((e = T0G_HIP(hipStreamCreateWithFlags(&dev->own_stream, hipStreamNonBlocking))) != hipSuccess)
+        return hip_fail(e, "hipStreamCreate");
+    dev->stream = dev->own_stream;
+    if ((e = T0G_HIP(hipModuleLoadData(&dev->module, t0g_hsaco_begin))) != hipSuccess) {
+        (void)hipStreamDestroy(dev->own_stream);
+        return hip_fail(e, "hipModuleLoadData(gfx950 GEMM code object)");
+    }
+    *out = dev.release();
+    return ok();
+}
+
+int t0g_device_close(t0g_device *dev) {
+    if (!dev) return ok();
+    (void)hipSetDevice(dev->ordinal);
+    if (!dev->poisoned) (void)hipStreamSynchronize(dev->stream);
+    if (dev->ws) (void)hipFree((void *)dev->ws);
+    for (uint64_t a : dev->allocations) (void)hipFree((void *)a);
+    for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
+    if (dev->module) (void)hipModuleUnload(dev->module);
+    if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
+    delete dev;
+    return ok();
+}
+
+int t0g_device_set_stream(t0g_device *dev, void *hip_stream) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    dev->stream = hip_stream ? (hipStream_t)hip_stream : dev->own_stream;
+    return ok();
+}
+
+int t0g_device_get_stream(t0g_device *dev, void **hip_stream) {
+    if (!dev || !hip_stream) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *hip_stream = (void *)dev->stream;
+    return ok();
+}
+
+int t0g_device_is_poisoned(t0g_device *dev, int *poisoned) {
+    if (!dev || !poisoned) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *poisoned = dev->poisoned ? 1 : 0;
+    return ok();
+}
+
+int t0g_alloc(t0g_device *dev, size_t bytes, uint64_t *addr) {
+    if (!dev || !addr) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *addr = 0;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    void *p = nullptr;
+    hipError_t e = T0G_HIP(hipMalloc(&p, bytes ? bytes : 1));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    dev->allocations.insert((uint64_t)p);
+    *addr = (uint64_t)p;
+    return ok();
+}
+
+int t0g_alloc_zero(t0g_device *dev, size_t bytes, uint64_t *addr) {
+    int rc = t0g_alloc(dev, bytes, addr);
+    if (rc) return rc;
+    return t0g_memset(dev, *addr, 0, bytes);
+}
+
+int t0g_free(t0g_device *dev, uint64_t addr) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (!dev->allocations.count(addr)) return fail(T0G_ERR_INVALID_ARG, "0x%llx was not allocated by t0g_alloc", (unsigned long long)addr);
+    (void)hipSetDevice(dev->ordinal);
+    if (!dev->poisoned) {
+        int rc = wait_stream(dev);   // the reference frees without waiting (src/kfd/mod.rs:1057-1081)
+        if (rc) return rc;
+    }
+    dev->allocations.erase(addr);
+    hipError_t e = T0G_HIP(hipFree((void *)addr));
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return ok();
+}
+
+int t0g_memcpy_h2d(t0g_device *dev, uint64_t dst, const void *src, size_t bytes) {
+    if (!dev || (!src && bytes)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipError_t e = T0G_HIP(hipMemcpyAsync((void *)dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemcpy H2D"));
+    if ((rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
+int t0g_memcpy_d2h(t0g_device *dev, void *dst, uint64_t src, size_t bytes) {
+    if (!dev || (!dst && bytes)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipError_t e = T0G_HIP(hipMemcpyAsync(dst, (const void *)src, bytes, hipMemcpyDeviceToHost, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemcpy D2H"));
+    if ((rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
+int t0g_memset(t0g_device *dev, uint64_t dst, int value, size_t bytes) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipError_t e = T0G_HIP(hipMemsetAsync((void *)dst, value, bytes, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemset"));
+    if ((rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
+static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, KernelKind kind, t0g_kernel **out) {
+    if (!dev || !cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *out = nullptr;
+    int rc = validate(cfg);
+    if (rc) return rc;
+    if (cfg->transpose != T0G_NT && cfg->transpose != T0G_NN)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "reference-layout kernels are NT or NN");
+    char name[128];
+    t0g_config_name(cfg, name, sizeof name);
+    std::string key = std::string(kind == KernelKind::TileGemm ? "tile:" : "gen:") + name;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    auto it = dev->kernel_cache.find(key);
+    if (it != dev->kernel_cache.end()) {
+        *out = it->second;
+        return ok();
+    }
+    std::unique_ptr<t0g_kernel> k(new t0g_kernel);
+    k->kind = kind;
+    k->cfg = *cfg;
+    k->wg[0] = cfg->wg_size;
+    k->lds = t0g_config_lds_total(cfg);
+    if (kind == KernelKind::GemmGen)
+        k->kernarg_size = cfg->epilogue != T0G_EPI_STORE_F32 ? 48 : 40;
+    else
+        k->kernarg_size = cfg->epilogue != T0G_EPI_STORE_F32 ? 52 : 44;
+    k->name = name;
+    *out = k.get();
+    dev->kernel_cache.emplace(key, k.get());
+    dev->kernels.push_back(std::move(k));
+    return ok();
+}
+
+int t0g_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out) {
+    return kernel_get_common(dev, cfg, KernelKind::GemmGen, out);
+}
+
+int t0g_tile_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out) {
+    return kernel_get_common(dev, cfg, KernelKind::TileGemm, out);
+}
+
+int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size, const char *symbol,
+                    const uint32_t workgroup_size[3], uint32_t lds_size, t0g_kernel **out) {
+    if (!dev || !code_object || !symbol || !workgroup_size || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    (void)size;
+    *out = nullptr;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipModule_t m = nullptr;
+    hipError_t e = T0G_HIP(hipModuleLoadData(&m, code_object));
+    if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+    hipFunction_t f = nullptr;
+    e = T0G_HIP(hipModuleGetFunction(&f, m, symbol));
+    if (e != hipSuccess) {
+        (void)hipModuleUnload(m);
+        return hip_fail(e, "hipModuleGetFunction");
+    }
+    dev->extra_modules.push_back(m);
+    std::unique_ptr<t0g_kernel> k(new t0g_kernel);
+    k->kind = KernelKind::Raw;
+    memset(&k->cfg, 0, sizeof k->cfg);
+    k->fn = f;
+    for (int i = 0; i < 3; i++) k->wg[i] = workgroup_size[i] ? workgroup_size[i] : 1;
+    k->lds = lds_size;
+    k->kernarg_size = 0;
+    k->name = symbol;
+    *out = k.get();
+    dev->kernels.push_back(std::move(k));
+    return ok();
+}
+
+int t0g_kernel_info(const t0g_kernel *kernel, uint32_t *wg_size, uint32_t *lds_size, uint32_t *kernarg_size,
+                    char *name, size_t name_len) {
+    if (!kernel) return fail(T0G_ERR_INVALID_ARG, "kernel is NULL");
+    if (wg_size) *wg_size = kernel->wg[0] * kernel->wg[1] * kernel->wg[2];
+    if (lds_size) *lds_size = kernel->lds;
+    if (kernarg_size) *kernarg_size = kernel->kernarg_size;
+    if (name && name_len) {
+        snprintf(name, name_len, "%s", kernel->name.c_str());
+    }
+    return ok();
+}
+
+static uint32_t rd_u32(const uint8_t *p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+static uint64_t rd_u64(const uint8_t *p) {
+    uint64_t v;
+    memcpy(&v, p, 8);
+    return v;
+}
+
+// Interpret reference-layout kernargs + a thread grid for a GEMM kernel handle
+// and launch the equivalent gfx950 GEMM (see t0g_kernel_get / t0g_tile_kernel_get).
+static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t grid[3], const uint8_t *ka,
+                         size_t len) {
+    const t0g_gemm_config &cfg = kn->cfg;
+    if (len < kn->kernarg_size)
+        return fail(T0G_ERR_INVALID_ARG, "kernargs are %zu bytes, %s needs %u", len, kn->name.c_str(),
+                    kn->kernarg_size);
+    const uint32_t wg = cfg.wg_size;
+    if (grid[0] % wg != 0) return fail(T0G_ERR_INVALID_ARG, "grid x=%u is not a multiple of wg_size %u", grid[0], wg);
+    if (grid[2] != 1) return fail(T0G_ERR_INVALID_ARG, "grid z must be 1 (got %u)", grid[2]);
+    const uint32_t sk = cfg_split(&cfg);
+    const uint32_t gx = grid[0] / wg, gy = grid[1];
+    if (gy % sk != 0) return fail(T0G_ERR_INVALID_ARG, "grid y=%u is not a multiple of split_k %u", gy, sk);
+    const uint32_t tiles_m = cfg.swap_grid ? gy / sk : gx;
+    const uint32_t tiles_n = cfg.swap_grid ? gx : gy / sk;
+    GemmOperands o;
+    memset(&o, 0, sizeof o);
+    o.a = rd_u64(ka + 0);
+    o.b = rd_u64(ka + 8);
+    o.c = rd_u64(ka + 16);
+    o.k = rd_u32(ka + 24);
+    o.n = rd_u32(ka + 28);
+    const uint32_t y_split_stride = rd_u32(ka + 36);
+    if (kn->kind == KernelKind::TileGemm) {
+        o.m = rd_u32(ka + 40);
+        if (cfg.epilogue != T0G_EPI_STORE_F32) o.bias = rd_u64(ka + 44);
+    } else if (cfg.epilogue != T0G_EPI_STORE_F32) {
+        o.bias = rd_u64(ka + 40);
+    }
+    if (o.m == 0) o.m = tiles_m * cfg.tile_m;   // gemm_gen kernargs carry no M: the grid covers it exactly
+    o.epilogue = cfg.epilogue;
+    o.lda = o.k;
+    o.ldb = cfg.transpose == T0G_NN ? o.n : o.k;
+    o.ldc = o.n;
+    if (sk > 1) {
+        if (y_split_stride == 0)
+            return fail(T0G_ERR_INVALID_ARG,
+                        "split_k=%u with y_split_stride=0 would make every K slice store to the same Y", sk);
+        if (o.k % (sk * kTileK) != 0)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "K=%u must be a multiple of tile_k*split_k=%u", o.k, sk * kTileK);
+        if ((uint64_t)y_split_stride < (uint64_t)o.m * o.n * 4)
+            return fail(T0G_ERR_INVALID_ARG, "y_split_stride=%u smaller than one M*N f32 plane", y_split_stride);
+        o.c_split_stride = y_split_stride;
+    }
+    int rc;
+    if ((rc = check_extent("X", o.m, o.lda))) return rc;
+    if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
+    const TileDef *tile = find_tile(cfg.tile_m, cfg.tile_n, cfg.tile_k, cfg.wg_size);
+    const bool aligned = operands_aligned(o.a, o.b, o.m, o.n, o.k, o.lda, o.ldb, cfg.transpose);
+    GemmPlan p;
+    if ((rc = make_plan(tile, cfg.transpose, false, aligned, o.m, o.n, o.k, sk, &p))) return rc;
+    if (p.tile != tile)   // the element-wise variant has a different tile: honour the caller's grid instead
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "tile %ux%u needs 16-byte aligned rows (K %% 8 == 0)", cfg.tile_m,
+                    cfg.tile_n);
+    p.tiles_m = tiles_m;
+    p.tiles_n = tiles_n;
+    p.splits = sk;
+    p.k_per_split = sk > 1 ? o.k / sk : (o.k ? o.k : kTileK);
+    if (tiles_m == 0 || tiles_n == 0) return ok();
+    return run_plan(dev, p, o, 0);
+}
+
+static int dispatch_common(t0g_device *dev, const t0g_kernel *kernel, const uint32_t grid[3], const void *ka,
+                           size_t len, bool sync) {
+    if (!dev || !kernel || !grid || (!ka && len)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if (kernel->kind == KernelKind::Raw) {
+        const uint32_t bx = kernel->wg[0], by = kernel->wg[1], bz = kernel->wg[2];
+        if (grid[0] % bx || grid[1] % by || grid[2] % bz)
+            return fail(T0G_ERR_INVALID_ARG, "grid (%u,%u,%u) is not a multiple of the workgroup", grid[0], grid[1],
+                        grid[2]);
+        std::vector<uint8_t> buf((const uint8_t *)ka, (const uint8_t *)ka + len);
+        size_t sz = len;
+        void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, buf.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                         HIP_LAUNCH_PARAM_END};
+        hipError_t e = T0G_HIP(hipModuleLaunchKernel(kernel->fn, grid[0] / bx, grid[1] / by, grid[2] / bz, bx, by, bz,
+                                                     kernel->lds, dev->stream, nullptr, extra));
+        if (e != hipSuccess) return poison(dev, hip_fail(e, "hipModuleLaunchKernel"));
+    } else {
+        rc = dispatch_gemm(dev, kernel, grid, (const uint8_t *)ka, len);
+        if (rc) return rc;
+    }
+    if (sync && (rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
+int t0g_dispatch(t0g_device *dev, const t0g_kernel *kernel, const uint32_t grid_threads[3], const void *kernargs,
+                 size_t kernargs_len) {
+    return dispatch_common(dev, kernel, grid_threads, kernargs, kernargs_len, true);
+}
+
+int t0g_dispatch_async(t0g_device *dev, const t0g_kernel *kernel, const uint32_t grid_threads[3],
+                       const void *kernargs, size_t kernargs_len) {
+    return dispatch_common(dev, kernel, grid_threads, kernargs, kernargs_len, false);
+}
+
+int t0g_wait_idle(t0g_device *dev) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if ((rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
+int t0g_gemm_workspace_size(const t0g_gemm_desc *d, size_t *bytes) {
+    if (!bytes) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    t0g_gemm_config cfg;
+    GemmPlan p;
+    GemmOperands o;
+    int rc = resolve_desc(d, &cfg, &p, &o);
+    if (rc) return rc;
+    *bytes = p.splits > 1 ? (size_t)p.splits * d->m * d->n * 4 : 0;
+    return ok();
+}
+
+int t0g_gemm_kernel_name(const t0g_gemm_desc *d, char *buf, size_t len) {
+    if (!buf || !len) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    t0g_gemm_config cfg;
+    GemmPlan p;
+    GemmOperands o;
+    int rc = resolve_desc(d, &cfg, &p, &o);
+    if (rc) return rc;
+    snprintf(buf, len, "%s", p.symbol.c_str());
+    return ok();
+}
+
+int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    t0g_gemm_config cfg;
+    GemmPlan p;
+    GemmOperands o;
+    int rc = resolve_desc(d, &cfg, &p, &o);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if ((rc = check_usable(dev))) return rc;
+    if (d->m == 0 || d->n == 0) return ok();
+    uint64_t ws = 0;
+    if (p.splits > 1) {
+        const size_t need = (size_t)p.splits * d->m * d->n * 4;
+        if (d->workspace) {
+            if (d->workspace_bytes < need)
+                return fail(T0G_ERR_INVALID_ARG, "workspace of %llu bytes, split-K needs %zu",
+                            (unsigned long long)d->workspace_bytes, need);
+            ws = d->workspace;
+        } else {
+            if ((rc = ensure_workspace(dev, need))) return rc;
+            ws = dev->ws;
+        }
+    }
+    if ((rc = run_plan(dev, p, o, ws))) return rc;
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,466 @@
+"""Python binding of libt0g (the MI355X bf16 GEMM path) over its C ABI.
+
+Mirrors the reference's GEMM call surface so that callers and tests read like
+the reference's own Rust code:
+
+    cfg = auto_select(m, k, n)                    # src/t0/gemm_gen.rs:320
+    gx, gy = compute_grid_auto(cfg, m, n)         # src/t0/gemm_gen.rs:402
+    ka = build_kernargs(x, wt, y, k, n, m, cfg)   # src/t0/gemm_gen.rs:414
+    rt = GpuRuntime.new()                         # src/ignis/gpu_context.rs:86
+    kern = rt.ensure_gemm_kernel(cfg)             # generate + compile + load
+    rt.dispatch(kern, [gx, gy, 1], ka)            # src/ignis/gpu_context.rs:264
+
+plus a typed one-shot `GpuRuntime.gemm(...)`.  Every compute call runs the
+gfx950 kernels in lib/libt0g.so; there is no CPU fallback: if the library is
+missing the import fails loudly.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libt0g.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()' "
+        f"or make -C t0-gpu_amd)")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+OK = 0
+ERR_INVALID_ARG = 1
+ERR_UNSUPPORTED_CONFIG = 2
+ERR_HIP = 3
+ERR_TIMEOUT = 4
+ERR_POISONED = 5
+ERR_NO_DEVICE = 6
+ERR_OUT_OF_MEMORY = 7
+
+NT, NN, TN, TT = 0, 1, 2, 3
+LAYOUTS = {"NT": NT, "NN": NN, "TN": TN, "TT": TT}
+EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
+F32, BF16 = 0, 1
+
+
+class T0gError(RuntimeError):
+    """A failed C-ABI call: `code` is the t0g_status, the message is t0g_last_error()."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"[t0g status {code}] {msg}")
+        self.code = code
+
+
+class GemmConfig(ctypes.Structure):
+    """GemmConfig (src/t0/gemm_gen.rs:56-84); split_k 0 means None."""
+
+    _fields_ = [
+        ("tile_m", ctypes.c_uint32),
+        ("tile_n", ctypes.c_uint32),
+        ("tile_k", ctypes.c_uint32),
+        ("wg_size", ctypes.c_uint32),
+        ("split_k", ctypes.c_uint32),
+        ("lds_pad", ctypes.c_uint32),
+        ("n_col_passes", ctypes.c_uint32),
+        ("use_lds", ctypes.c_uint8),
+        ("double_buffer", ctypes.c_uint8),
+        ("swap_grid", ctypes.c_uint8),
+        ("wgp_mode", ctypes.c_uint8),
+        ("transpose", ctypes.c_uint32),
+        ("epilogue", ctypes.c_uint32),
+    ]
+
+    @staticmethod
+    def preset(name):
+        cfg = GemmConfig()
+        _check(_lib.t0g_config_preset(name.encode(), ctypes.byref(cfg)))
+        return cfg
+
+    def copy(self, **changes):
+        c = GemmConfig()
+        ctypes.memmove(ctypes.byref(c), ctypes.byref(self), ctypes.sizeof(GemmConfig))
+        for k, v in changes.items():
+            setattr(c, k, v)
+        return c
+
+    def validate(self):
+        _check(_lib.t0g_config_validate(ctypes.byref(self)))
+
+    def n_waves(self):
+        return _lib.t0g_config_n_waves(ctypes.byref(self))
+
+    def lds_total(self):
+        return _lib.t0g_config_lds_total(ctypes.byref(self))
+
+    def name(self):
+        buf = ctypes.create_string_buffer(128)
+        _check(_lib.t0g_config_name(ctypes.byref(self), buf, len(buf)))
+        return buf.value.decode()
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+    def __repr__(self):
+        return f"GemmConfig({self.name()})"
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("a", ctypes.c_uint64),
+        ("b", ctypes.c_uint64),
+        ("c", ctypes.c_uint64),
+        ("bias", ctypes.c_uint64),
+        ("workspace", ctypes.c_uint64),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("m", ctypes.c_uint32),
+        ("n", ctypes.c_uint32),
+        ("k", ctypes.c_uint32),
+        ("lda", ctypes.c_uint32),
+        ("ldb", ctypes.c_uint32),
+        ("ldc", ctypes.c_uint32),
+        ("transpose", ctypes.c_uint32),
+        ("out_dtype", ctypes.c_uint32),
+        ("epilogue", ctypes.c_uint32),
+        ("split_k", ctypes.c_uint32),
+        ("config", ctypes.POINTER(GemmConfig)),
+    ]
+
+
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_p = ctypes.c_void_p
+_cfgp = ctypes.POINTER(GemmConfig)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+def _sig(name, restype, *argtypes):
+    f = getattr(_lib, name)
+    f.restype = restype
+    f.argtypes = list(argtypes)
+    return f
+
+
+_sig("t0g_last_error", ctypes.c_char_p)
+_sig("t0g_version", ctypes.c_char_p)
+_sig("t0g_config_preset", ctypes.c_int, ctypes.c_char_p, _cfgp)
+_sig("t0g_config_validate", ctypes.c_int, _cfgp)
+_sig("t0g_config_n_waves", _u32, _cfgp)
+_sig("t0g_config_lds_total", _u32, _cfgp)
+_sig("t0g_config_name", ctypes.c_int, _cfgp, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_auto_select", ctypes.c_int, _u32, _u32, _u32, _cfgp)
+_sig("t0g_tile_auto_select", ctypes.c_int, _u32, _u32, _u32, _u32, _cfgp)
+_sig("t0g_compute_grid", ctypes.c_int, _cfgp, _u32, _u32, _u32p, _u32p)
+_sig("t0g_compute_grid_split_k", ctypes.c_int, _cfgp, _u32, _u32, _u32, _u32p, _u32p)
+_sig("t0g_compute_grid_auto", ctypes.c_int, _cfgp, _u32, _u32, _u32p, _u32p)
+_sig("t0g_tile_compute_grid", ctypes.c_int, _cfgp, _u32, _u32, _u32p)
+_sig("t0g_build_kernargs", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, ctypes.c_char_p)
+_sig("t0g_build_kernargs_with_bias", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, _u64,
+     ctypes.c_char_p)
+_sig("t0g_build_kernargs_m", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, ctypes.c_char_p)
+_sig("t0g_auto_select_backward_data", ctypes.c_int, _u32, _u32, _u32, _cfgp)
+_sig("t0g_auto_select_backward_weight", ctypes.c_int, _u32, _u32, _u32, _cfgp)
+_sig("t0g_build_kernargs_backward_data", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp,
+     ctypes.c_char_p)
+_sig("t0g_build_kernargs_backward_weight", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp,
+     ctypes.c_char_p)
+_sig("t0g_compute_grid_backward_data", ctypes.c_int, _cfgp, _u32, _u32, _u32p, _u32p)
+_sig("t0g_compute_grid_backward_weight", ctypes.c_int, _cfgp, _u32, _u32, _u32p, _u32p)
+_sig("t0g_device_count", ctypes.c_int, ctypes.POINTER(ctypes.c_int))
+_sig("t0g_device_open", ctypes.c_int, ctypes.c_int, ctypes.POINTER(_p))
+_sig("t0g_device_close", ctypes.c_int, _p)
+_sig("t0g_device_set_stream", ctypes.c_int, _p, _p)
+_sig("t0g_device_get_stream", ctypes.c_int, _p, ctypes.POINTER(_p))
+_sig("t0g_device_is_poisoned", ctypes.c_int, _p, ctypes.POINTER(ctypes.c_int))
+_sig("t0g_alloc", ctypes.c_int, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
+_sig("t0g_alloc_zero", ctypes.c_int, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
+_sig("t0g_free", ctypes.c_int, _p, _u64)
+_sig("t0g_memcpy_h2d", ctypes.c_int, _p, _u64, _p, ctypes.c_size_t)
+_sig("t0g_memcpy_d2h", ctypes.c_int, _p, _p, _u64, ctypes.c_size_t)
+_sig("t0g_memset", ctypes.c_int, _p, _u64, ctypes.c_int, ctypes.c_size_t)
+_sig("t0g_kernel_get", ctypes.c_int, _p, _cfgp, ctypes.POINTER(_p))
+_sig("t0g_tile_kernel_get", ctypes.c_int, _p, _cfgp, ctypes.POINTER(_p))
+_sig("t0g_kernel_load", ctypes.c_int, _p, _p, ctypes.c_size_t, ctypes.c_char_p, _u32p, _u32,
+     ctypes.POINTER(_p))
+_sig("t0g_kernel_info", ctypes.c_int, _p, _u32p, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_dispatch", ctypes.c_int, _p, _p, _u32p, _p, ctypes.c_size_t)
+_sig("t0g_dispatch_async", ctypes.c_int, _p, _p, _u32p, _p, ctypes.c_size_t)
+_sig("t0g_wait_idle", ctypes.c_int, _p)
+_sig("t0g_gemm", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
+_sig("t0g_gemm_workspace_size", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_size_t))
+_sig("t0g_gemm_kernel_name", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
+_sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
+
+
+def _check(rc):
+    if rc != OK:
+        raise T0gError(rc, _lib.t0g_last_error().decode(errors="replace"))
+
+
+def last_error():
+    return _lib.t0g_last_error().decode(errors="replace")
+
+
+def version():
+    return _lib.t0g_version().decode()
+
+
+def library():
+    """The loaded ctypes.CDLL (for symbol-level tests)."""
+    return _lib
+
+
+# ---- selection, grids, kernargs (host only) ---------------------------------
+
+def auto_select(m, k, n):
+    cfg = GemmConfig()
+    _check(_lib.t0g_auto_select(m, k, n, ctypes.byref(cfg)))
+    return cfg
+
+
+def tile_auto_select(m, k, n, transpose=NT):
+    cfg = GemmConfig()
+    _check(_lib.t0g_tile_auto_select(m, k, n, transpose, ctypes.byref(cfg)))
+    return cfg
+
+
+def _grid2(fn, *args):
+    gx, gy = ctypes.c_uint32(), ctypes.c_uint32()
+    _check(fn(*args, ctypes.byref(gx), ctypes.byref(gy)))
+    return gx.value, gy.value
+
+
+def compute_grid(cfg, m, n):
+    return _grid2(_lib.t0g_compute_grid, ctypes.byref(cfg), m, n)
+
+
+def compute_grid_split_k(cfg, m, n, split_k):
+    return _grid2(_lib.t0g_compute_grid_split_k, ctypes.byref(cfg), m, n, split_k)
+
+
+def compute_grid_auto(cfg, m, n):
+    return _grid2(_lib.t0g_compute_grid_auto, ctypes.byref(cfg), m, n)
+
+
+def tile_compute_grid(cfg, m, n):
+    g = (ctypes.c_uint32 * 3)()
+    _check(_lib.t0g_tile_compute_grid(ctypes.byref(cfg), m, n, g))
+    return [g[0], g[1], g[2]]
+
+
+def build_kernargs(x, wt, y, k, n, m, cfg):
+    buf = ctypes.create_string_buffer(40)
+    _check(_lib.t0g_build_kernargs(x, wt, y, k, n, m, ctypes.byref(cfg), buf))
+    return buf.raw
+
+
+def build_kernargs_with_bias(x, wt, y, k, n, m, cfg, bias):
+    buf = ctypes.create_string_buffer(48)
+    _check(_lib.t0g_build_kernargs_with_bias(x, wt, y, k, n, m, ctypes.byref(cfg), bias, buf))
+    return buf.raw
+
+
+def build_kernargs_m(x, wt, y, k, n, m, cfg):
+    buf = ctypes.create_string_buffer(44)
+    _check(_lib.t0g_build_kernargs_m(x, wt, y, k, n, m, ctypes.byref(cfg), buf))
+    return buf.raw
+
+
+def auto_select_backward_data(m, n_orig, k_orig):
+    cfg = GemmConfig()
+    _check(_lib.t0g_auto_select_backward_data(m, n_orig, k_orig, ctypes.byref(cfg)))
+    return cfg
+
+
+def auto_select_backward_weight(m, n_orig, k_orig):
+    cfg = GemmConfig()
+    _check(_lib.t0g_auto_select_backward_weight(m, n_orig, k_orig, ctypes.byref(cfg)))
+    return cfg
+
+
+def build_kernargs_backward_data(dy, w, dx, m, n_orig, k_orig, cfg):
+    buf = ctypes.create_string_buffer(40)
+    _check(_lib.t0g_build_kernargs_backward_data(dy, w, dx, m, n_orig, k_orig, ctypes.byref(cfg), buf))
+    return buf.raw
+
+
+def build_kernargs_backward_weight(dy_t, x_t, dw, m, n_orig, k_orig, cfg):
+    buf = ctypes.create_string_buffer(40)
+    _check(_lib.t0g_build_kernargs_backward_weight(dy_t, x_t, dw, m, n_orig, k_orig, ctypes.byref(cfg), buf))
+    return buf.raw
+
+
+def compute_grid_backward_data(cfg, m, k_orig):
+    return _grid2(_lib.t0g_compute_grid_backward_data, ctypes.byref(cfg), m, k_orig)
+
+
+def compute_grid_backward_weight(cfg, n_orig, k_orig):
+    return _grid2(_lib.t0g_compute_grid_backward_weight, ctypes.byref(cfg), n_orig, k_orig)
+
+
+def gemm_desc(a, b, c, m, n, k, transpose=NT, out_dtype=F32, lda=0, ldb=0, ldc=0, split_k=0,
+              epilogue=EPI_STORE_F32, bias=0, workspace=0, workspace_bytes=0, config=None):
+    d = GemmDesc()
+    d.a, d.b, d.c, d.bias = a, b, c, bias
+    d.workspace, d.workspace_bytes = workspace, workspace_bytes
+    d.m, d.n, d.k = m, n, k
+    d.lda, d.ldb, d.ldc = lda, ldb, ldc
+    d.transpose = LAYOUTS[transpose] if isinstance(transpose, str) else transpose
+    d.out_dtype = out_dtype
+    d.epilogue = epilogue
+    d.split_k = split_k
+    d.config = ctypes.pointer(config) if config is not None else None
+    return d
+
+
+def gemm_workspace_size(desc):
+    n = ctypes.c_size_t()
+    _check(_lib.t0g_gemm_workspace_size(ctypes.byref(desc), ctypes.byref(n)))
+    return n.value
+
+
+def gemm_kernel_name(desc):
+    buf = ctypes.create_string_buffer(128)
+    _check(_lib.t0g_gemm_kernel_name(ctypes.byref(desc), buf, len(buf)))
+    return buf.value.decode()
+
+
+def debug_fail_hip_call(n):
+    _check(_lib.t0g_debug_fail_hip_call(n))
+
+
+def set_wait_timeout_ms(ms):
+    _check(_lib.t0g_set_wait_timeout_ms(ms))
+
+
+def device_count():
+    n = ctypes.c_int()
+    _check(_lib.t0g_device_count(ctypes.byref(n)))
+    return n.value
+
+
+class Kernel:
+    """A GpuKernel handle (owned by its GpuRuntime)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def info(self):
+        wg, lds, ka = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        name = ctypes.create_string_buffer(128)
+        _check(_lib.t0g_kernel_info(self.handle, ctypes.byref(wg), ctypes.byref(lds), ctypes.byref(ka), name,
+                                    len(name)))
+        return {"wg_size": wg.value, "lds_size": lds.value, "kernarg_size": ka.value, "name": name.value.decode()}
+
+
+class GpuRuntime:
+    """GpuRuntime (src/ignis/gpu_context.rs:86-147) over one HIP device."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def new(ordinal=0):
+        h = ctypes.c_void_p()
+        _check(_lib.t0g_device_open(ordinal, ctypes.byref(h)))
+        return GpuRuntime(h)
+
+    def close(self):
+        if self.handle:
+            _check(_lib.t0g_device_close(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def set_stream(self, hip_stream_ptr):
+        _check(_lib.t0g_device_set_stream(self.handle, ctypes.c_void_p(hip_stream_ptr or None)))
+
+    def stream(self):
+        s = ctypes.c_void_p()
+        _check(_lib.t0g_device_get_stream(self.handle, ctypes.byref(s)))
+        return s.value
+
+    def is_poisoned(self):
+        v = ctypes.c_int()
+        _check(_lib.t0g_device_is_poisoned(self.handle, ctypes.byref(v)))
+        return bool(v.value)
+
+    # memory (src/ignis/gpu_context.rs:437-487, src/kfd/mod.rs:947-1055)
+    def alloc(self, nbytes):
+        a = ctypes.c_uint64()
+        _check(_lib.t0g_alloc(self.handle, nbytes, ctypes.byref(a)))
+        return a.value
+
+    def alloc_zero(self, nbytes):
+        a = ctypes.c_uint64()
+        _check(_lib.t0g_alloc_zero(self.handle, nbytes, ctypes.byref(a)))
+        return a.value
+
+    def free(self, addr):
+        _check(_lib.t0g_free(self.handle, addr))
+
+    def write(self, addr, array):
+        """Host numpy array -> device (GpuBuffer::write)."""
+        import numpy as np
+        arr = np.ascontiguousarray(array)
+        _check(_lib.t0g_memcpy_h2d(self.handle, addr, arr.ctypes.data, arr.nbytes))
+
+    def read(self, addr, shape, dtype):
+        """Device -> new host numpy array (GpuBuffer::read)."""
+        import numpy as np
+        out = np.empty(shape, dtype=dtype)
+        _check(_lib.t0g_memcpy_d2h(self.handle, out.ctypes.data, addr, out.nbytes))
+        return out
+
+    def upload(self, array):
+        import numpy as np
+        arr = np.ascontiguousarray(array)
+        addr = self.alloc(arr.nbytes)
+        self.write(addr, arr)
+        return addr
+
+    def memset(self, addr, value, nbytes):
+        _check(_lib.t0g_memset(self.handle, addr, value, nbytes))
+
+    # kernels and dispatch
+    def ensure_gemm_kernel(self, cfg):
+        h = ctypes.c_void_p()
+        _check(_lib.t0g_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        return Kernel(h)
+
+    def ensure_tile_kernel(self, cfg):
+        h = ctypes.c_void_p()
+        _check(_lib.t0g_tile_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        return Kernel(h)
+
+    def load_kernel(self, code_object, symbol, workgroup_size, lds_size=0):
+        h = ctypes.c_void_p()
+        wg = (ctypes.c_uint32 * 3)(*workgroup_size)
+        buf = ctypes.create_string_buffer(bytes(code_object), len(code_object))
+        _check(_lib.t0g_kernel_load(self.handle, buf, len(code_object), symbol.encode(), wg, lds_size,
+                                    ctypes.byref(h)))
+        return Kernel(h)
+
+    def _dispatch(self, fn, kernel, grid, kernargs):
+        g = (ctypes.c_uint32 * 3)(*grid)
+        buf = ctypes.create_string_buffer(bytes(kernargs), len(kernargs))
+        _check(fn(self.handle, kernel.handle, g, buf, len(kernargs)))
+
+    def dispatch(self, kernel, grid, kernargs):
+        self._dispatch(_lib.t0g_dispatch, kernel, grid, kernargs)
+
+    def dispatch_async(self, kernel, grid, kernargs):
+        self._dispatch(_lib.t0g_dispatch_async, kernel, grid, kernargs)
+
+    def wait_idle(self):
+        _check(_lib.t0g_wait_idle(self.handle))
+
+    def gemm_desc(self, desc):
+        _check(_lib.t0g_gemm(self.handle, ctypes.byref(desc)))
+
+    def gemm(self, a, b, c, m, n, k, **kw):
+        """Enqueue C = op(A) op(B) on the device stream (asynchronous)."""
+        self.gemm_desc(gemm_desc(a, b, c, m, n, k, **kw))

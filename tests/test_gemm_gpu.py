@@ -1,0 +1,456 @@
+"""Parity of the gfx950 GEMM kernels with the CPU oracle, through the C ABI.
+
+Gate, on the fp32 result: relF <= 5e-3 and
+max|d| <= 1e-2 * sqrt(K/256).  bf16 output is checked bit-exactly against
+round-to-nearest-even of the same kernel's fp32 result.  Inputs come from the
+reference's own generators (restated in the oracle) with its seeds.
+Full-size cases (4096^3, 8192^3, the MLP step) compare sampled output rows
+with the oracle and check size-independent properties on the whole matrix.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as o
+import t0g
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def rt():
+    r = t0g.GpuRuntime.new(0)
+    yield r
+    r.close()
+
+
+class Buffers:
+    """Device buffers freed at the end of a test."""
+
+    def __init__(self, rt):
+        self.rt = rt
+        self.addrs = []
+
+    def up(self, arr):
+        a = self.rt.upload(arr)
+        self.addrs.append(a)
+        return a
+
+    def alloc(self, nbytes, fill=None):
+        a = self.rt.alloc(nbytes)
+        self.addrs.append(a)
+        if fill is not None:
+            self.rt.memset(a, fill, nbytes)
+        return a
+
+    def free(self):
+        for a in self.addrs:
+            self.rt.free(a)
+        self.addrs = []
+
+
+@pytest.fixture
+def bufs(rt):
+    b = Buffers(rt)
+    yield b
+    b.free()
+
+
+def stored_operands(layout, a_mk, b_nk):
+    """From op(A) as [M][K] and op(B)^T as [N][K], the arrays as stored for `layout`."""
+    a_st = a_mk if layout in ("NT", "NN") else np.ascontiguousarray(a_mk.T)
+    b_st = b_nk if layout in ("NT", "TT") else np.ascontiguousarray(b_nk.T)
+    return a_st, b_st
+
+
+def run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, out=t0g.F32, **kw):
+    a = bufs.up(a_st)
+    b = bufs.up(b_st)
+    esz = 4 if out == t0g.F32 else 2
+    ldc = kw.pop("ldc", 0) or n
+    c = bufs.alloc(m * ldc * esz, fill=0)
+    rt.gemm(a, b, c, m, n, k, transpose=layout, out_dtype=out, ldc=ldc, **kw)
+    rt.wait_idle()
+    raw = rt.read(c, (m, ldc), np.float32 if out == t0g.F32 else np.uint16)
+    return raw[:, :n]
+
+
+def check_parity(c_gpu, c_ref, k, label):
+    ok, relf, maxabs, bound = o.parity(c_gpu, c_ref, k)
+    _log(f"[parity] {label}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
+    assert ok, f"{label}: relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
+
+
+PRESETS = ["tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
+
+
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+@pytest.mark.parametrize("preset", PRESETS + [None])
+def test_c1_256_cubed_all_layouts(rt, bufs, layout, preset):
+    """256^3, U(-1,1) xorshift data with the seeds of
+    examples/test_gemm_correctness.rs:128-129; fp32 and bf16 output."""
+    m = n = k = 256
+    _log(f"[case] c1 layout={layout} preset={preset}")
+    a_mk = o.rand_bf16_xorshift(m * k, m * 1000 + k).reshape(m, k)
+    b_nk = o.rand_bf16_xorshift(n * k, n * 2000 + k).reshape(n, k)
+    ref = o.gemm_nt_naive(a_mk, b_nk, m, k, n)
+    a_st, b_st = stored_operands(layout, a_mk, b_nk)
+    cfg = t0g.GemmConfig.preset(preset) if preset else None
+    c32 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, config=cfg)
+    check_parity(c32, ref, k, f"256^3 {layout} {preset}")
+    c16 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, out=t0g.BF16, config=cfg)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c32)), "bf16 output != RNE(fp32 output)"
+
+
+def test_torch_golden_through_gpu(rt, bufs):
+    tr = os.path.join(GOLDEN, "torch_ref")
+    x = np.fromfile(os.path.join(tr, "x.bin"), dtype=np.uint16).reshape(64, 256)
+    w = np.fromfile(os.path.join(tr, "w_gate.bin"), dtype=np.uint16).reshape(512, 256)
+    ref = np.fromfile(os.path.join(tr, "h_gate_f32ref.bin"), dtype=np.float32).reshape(64, 512)
+    c = run_gemm(rt, bufs, "NT", x, w, 64, 512, 256)
+    check_parity(c, ref, 256, "torch golden h_gate")
+    assert np.abs(c - ref).max() < 1e-5
+    s = np.fromfile(os.path.join(tr, "swiglu_bf16_trunc.bin"), dtype=np.uint16).reshape(64, 512)
+    wd = np.fromfile(os.path.join(tr, "w_down.bin"), dtype=np.uint16).reshape(256, 512)
+    refy = np.fromfile(os.path.join(tr, "y_bf16_f32acc.bin"), dtype=np.float32).reshape(64, 256)
+    cy = run_gemm(rt, bufs, "NT", s, wd, 64, 256, 512)
+    assert np.abs(cy - refy).max() < 1e-5
+
+
+SUITE = [(128, 128, 128), (256, 256, 256), (128, 1024, 512), (256, 512, 128), (512, 512, 512),
+         (1024, 1024, 1024), (33, 100, 50), (129, 65, 17), (100, 300, 200), (1000, 768, 512),
+         (1, 1, 1), (7, 9, 3), (300, 8, 264), (64, 4096, 64)]
+
+
+@pytest.mark.parametrize("m,k,n", SUITE)
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN"])
+def test_tile_suite_shapes(rt, bufs, m, k, n, layout):
+    """Aligned and non-aligned shapes of src/t0/test_tile_gemm_suite.rs:179-208
+    (make_bf16 data, seeds 42+m / 137+n), plus degenerate ones."""
+    _log(f"[case] suite {m}x{k}x{n} {layout}")
+    a_mk = o.make_bf16_suite(m * k, 42 + m).reshape(m, k)
+    b_nk = o.make_bf16_suite(n * k, 137 + n).reshape(n, k)
+    ref = o.gemm_nt_naive(a_mk, b_nk, m, k, n)
+    a_st, b_st = stored_operands(layout, a_mk, b_nk)
+    c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k)
+    check_parity(c, ref, k, f"suite {m}x{k}x{n} {layout}")
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+@pytest.mark.parametrize("m", [1, 17, 64, 100, 250])
+def test_no_writes_outside_the_output(rt, bufs, preset, m):
+    """Sentinel test after src/t0/tile_boundary_tests.rs:84-145: rows >= M and
+    columns >= N of a padded C (ldc > N) must keep the sentinel -9999.0."""
+    k, n, ldc = 96, 72, 80
+    _log(f"[case] sentinel {preset} m={m}")
+    a_mk = o.rand_bf16_lcg(m * k, 42 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 137 + n).reshape(n, k)
+    ref = o.gemm_nt_naive(a_mk, b_nk, m, k, n)
+    rows_alloc = m + 300
+    sentinel = np.full((rows_alloc, ldc), -9999.0, dtype=np.float32)
+    a = bufs.up(a_mk)
+    b = bufs.up(b_nk)
+    c = bufs.up(sentinel)
+    rt.gemm(a, b, c, m, n, k, transpose="NT", ldc=ldc, config=t0g.GemmConfig.preset(preset))
+    rt.wait_idle()
+    got = rt.read(c, (rows_alloc, ldc), np.float32)
+    check_parity(got[:m, :n], ref, k, f"sentinel {preset} m={m}")
+    assert np.all(got[m:] == -9999.0), "rows >= M were written"
+    assert np.all(got[:m, n:] == -9999.0), "columns >= N were written"
+
+
+def test_all_ones_known_answer(rt, bufs):
+    """examples/hello_gemm_gen.rs:72-133: bf16(1.0) inputs give C = K exactly."""
+    for (m, k, n) in [(256, 4096, 256), (128, 1024, 4096), (512, 512, 512)]:
+        ones_a = np.full((m, k), 0x3F80, dtype=np.uint16)
+        ones_b = np.full((n, k), 0x3F80, dtype=np.uint16)
+        c = run_gemm(rt, bufs, "NT", ones_a, ones_b, m, n, k)
+        assert np.all(c == float(k)), (m, k, n)
+        c = run_gemm(rt, bufs, "NT", ones_a, ones_b, m, n, k, split_k=4)
+        assert np.all(c == float(k)), (m, k, n, "split-K")
+
+
+def test_k_zero_gives_zero_plus_bias(rt, bufs):
+    m, n = 64, 96
+    a = bufs.alloc(16)
+    b = bufs.alloc(16)
+    bias = np.linspace(-1, 1, n).astype(np.float32)
+    bp = bufs.up(bias)
+    c = bufs.alloc(m * n * 4, fill=0x7F)
+    rt.gemm(a, b, c, m, n, 0, transpose="NT", lda=8, ldb=8, epilogue=t0g.EPI_BIAS_ADD, bias=bp)
+    rt.wait_idle()
+    got = rt.read(c, (m, n), np.float32)
+    assert np.array_equal(got, np.broadcast_to(bias, (m, n)))
+
+
+def test_c4a_thin(rt, bufs):
+    """BASELINE config 4a: M=128, K=4096, N=4096, LCG data (tile_boundary_tests.rs:42-49)."""
+    m, k, n = 128, 4096, 4096
+    a_mk = o.rand_bf16_lcg(m * k, 42 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 137 + n).reshape(n, k)
+    ref = o.gemm("NT", a_mk, b_nk, m, n, k)
+    for layout in ("NT", "NN"):
+        a_st, b_st = stored_operands(layout, a_mk, b_nk)
+        c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k)
+        check_parity(c, ref, k, f"thin 128x4096x4096 {layout}")
+
+
+@pytest.mark.parametrize("split_k", [0, 8, 16, 32, 64])
+def test_c4b_split_k(rt, bufs, split_k):
+    """BASELINE config 4b: M=N=256, K=32768, fp32 partial planes reduced in plane order."""
+    m, k, n = 256, 32768, 256
+    _log(f"[case] split-K sk={split_k}")
+    a_mk = o.rand_bf16_lcg(m * k, 42 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 137 + n).reshape(n, k)
+    ref = o.gemm("NT", a_mk, b_nk, m, n, k)
+    c1 = run_gemm(rt, bufs, "NT", a_mk, b_nk, m, n, k, split_k=split_k)
+    check_parity(c1, ref, k, f"split-K 256x32768x256 sk={split_k}")
+    c2 = run_gemm(rt, bufs, "NT", a_mk, b_nk, m, n, k, split_k=split_k)
+    assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32)), "split-K result is not deterministic"
+    c16 = run_gemm(rt, bufs, "NT", a_mk, b_nk, m, n, k, split_k=split_k, out=t0g.BF16)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c1))
+
+
+def _randn_pair(m, n, k, seed_a=2, seed_b=3):
+    a = o.randn_bf16(m * k, seed_a, 0.02)
+    b = o.randn_bf16(k * n, seed_b, 0.02)
+    return a, b
+
+
+SAMPLE_ROWS = 48
+
+
+def _sample_rows(m):
+    rng = np.random.default_rng(m)
+    rows = set([0, 1, m - 1, m // 2, 255, 256]) | set(rng.integers(0, m, SAMPLE_ROWS).tolist())
+    return np.array(sorted(r for r in rows if r < m))
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT"])
+def test_c2_4096_cubed(rt, bufs, layout):
+    """4096^3, N(0,1)*0.02.  Sampled rows against the oracle,
+    whole-matrix bf16 == RNE(fp32)."""
+    m = n = k = 4096
+    _log(f"[case] 4096^3 {layout}")
+    a, b = _randn_pair(m, n, k)   # A as stored [M][K]; B as stored [K][N] (NN) or [N][K] (NT)
+    rows = _sample_rows(m)
+    ref = o.gemm_rows(layout, a, b, m, n, k, rows)
+    c32 = run_gemm(rt, bufs, layout, a, b, m, n, k)
+    check_parity(c32[rows], ref, k, f"4096^3 {layout} sampled rows")
+    c16 = run_gemm(rt, bufs, layout, a, b, m, n, k, out=t0g.BF16)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c32))
+
+
+def test_c3_8192_cubed(rt, bufs):
+    """8192^3 NN, N(0,1)*0.02, sampled rows + bf16 consistency."""
+    m = n = k = 8192
+    _log("[case] 8192^3 NN")
+    a, b = _randn_pair(m, n, k, 4, 5)
+    rows = _sample_rows(m)[:24]
+    ref = o.gemm_rows("NN", a, b, m, n, k, rows)
+    c32 = run_gemm(rt, bufs, "NN", a, b, m, n, k)
+    check_parity(c32[rows], ref, k, "8192^3 NN sampled rows")
+    c16 = run_gemm(rt, bufs, "NN", a, b, m, n, k, out=t0g.BF16)
+    assert np.array_equal(c16[::7], o.f32_to_bf16_rne(c32[::7]))
+
+
+def test_c5_mlp_step(rt, bufs):
+    """2-layer MLP step, batch 1024, 4096 -> 11008 -> 4096.
+    He-init weights (src/ignis/nn/linear.rs:36-43, [in, out] layout, RNE to bf16
+    as src/ignis/ops/bf16_matmul.rs:357-384 does).  Forward H = X W1, Y = H W2 (NN);
+    backward dH = dY W2^T, dX = dH W1^T (NT on the stored weights), dW2 = H^T dY,
+    dW1 = X^T dH (TN) -- no host transposes."""
+    bsz, d_in, d_hid = 1024, 4096, 11008
+    _log("[case] MLP step")
+    x = o.randn_bf16(bsz * d_in, 7, 1.0).reshape(bsz, d_in)
+    w1 = o.f32_to_bf16_rne(o.linear_init_f32(d_in, d_hid, seed=42))        # [4096, 11008]
+    w2 = o.f32_to_bf16_rne(o.linear_init_f32(d_hid, d_in, seed=43))        # [11008, 4096]
+    dy = o.randn_bf16(bsz * d_in, 8, 0.02).reshape(bsz, d_in)
+    rows = _sample_rows(bsz)[:16]
+
+    h32 = run_gemm(rt, bufs, "NN", x, w1, bsz, d_hid, d_in)
+    check_parity(h32[rows], o.gemm_rows("NN", x, w1, bsz, d_hid, d_in, rows), d_in, "MLP H = X W1")
+    h = o.f32_to_bf16_rne(h32)
+    y32 = run_gemm(rt, bufs, "NN", h, w2, bsz, d_in, d_hid)
+    check_parity(y32[rows], o.gemm_rows("NN", h, w2, bsz, d_in, d_hid, rows), d_hid, "MLP Y = H W2")
+    dh32 = run_gemm(rt, bufs, "NT", dy, w2, bsz, d_hid, d_in)
+    check_parity(dh32[rows], o.gemm_rows("NT", dy, w2, bsz, d_hid, d_in, rows), d_in, "MLP dH = dY W2^T")
+    dh = o.f32_to_bf16_rne(dh32)
+    dx32 = run_gemm(rt, bufs, "NT", dh, w1, bsz, d_in, d_hid)
+    check_parity(dx32[rows], o.gemm_rows("NT", dh, w1, bsz, d_in, d_hid, rows), d_hid, "MLP dX = dH W1^T")
+    wrows = np.array([0, 1, 777, 4095, 5000, 11007])
+    dw2 = run_gemm(rt, bufs, "TN", h, dy, d_hid, d_in, bsz)
+    check_parity(dw2[wrows], o.gemm_rows("TN", h, dy, d_hid, d_in, bsz, wrows), bsz, "MLP dW2 = H^T dY")
+    dw1 = run_gemm(rt, bufs, "TN", x, dh, d_in, d_hid, bsz)
+    check_parity(dw1[wrows[:4]], o.gemm_rows("TN", x, dh, d_in, d_hid, bsz, wrows[:4]), bsz, "MLP dW1 = X^T dH")
+
+
+# ---- the reference's own call sequence: select -> kernel -> kernargs -> grid -> dispatch ----
+
+REF_CFGS = [("tile_64x64_k64", 0), ("tile_128x128_k64", 0), ("tile_128x128_k64", 2), ("tile_64x64_k64", 4),
+            ("tile_64x64_k64", 8), ("tile_256x256_k64", 0)]
+REF_SIZES = [(64, 64, 64), (128, 128, 128), (256, 256, 256), (64, 256, 64), (128, 1024, 256), (256, 512, 512)]
+
+
+@pytest.mark.parametrize("preset,sk", REF_CFGS)
+def test_reference_dispatch_sequence(rt, bufs, preset, sk):
+    """examples/test_gemm_correctness.rs:118-261: build_kernargs + compute_grid_auto +
+    dispatch, split-K planes at Y + s*M*N*4 summed on the host in plane order."""
+    cfg = t0g.GemmConfig.preset(preset).copy(split_k=sk)
+    kern = rt.ensure_gemm_kernel(cfg)
+    assert kern.info()["kernarg_size"] == 40
+    for (m, k, n) in REF_SIZES:
+        if m % cfg.tile_m or n % cfg.tile_n or k % (64 * max(sk, 1)):
+            continue   # gemm_gen's divisibility contract
+        _log(f"[case] ref dispatch {preset} sk={sk} {m}x{k}x{n}")
+        x = o.rand_bf16_xorshift(m * k, m * 1000 + k)
+        wt = o.rand_bf16_xorshift(n * k, n * 2000 + k)
+        ref = o.gemm_nt_naive(x, wt, m, k, n)
+        xa, wa = bufs.up(x), bufs.up(wt)
+        planes = max(sk, 1)
+        y = bufs.alloc(m * n * 4 * planes, fill=0)
+        ka = t0g.build_kernargs(xa, wa, y, k, n, m, cfg)
+        gx, gy = t0g.compute_grid_auto(cfg, m, n)
+        rt.dispatch(kern, [gx, gy, 1], ka)
+        p = rt.read(y, (planes, m, n), np.float32)
+        got = o.splitk_reduce(p)
+        check_parity(got, ref, k, f"ref dispatch {preset} sk={sk} {m}x{k}x{n}")
+        if planes > 1:
+            exp = np.stack([o.gemm_krange("NT", x, wt, m, n, k, s * k // planes, (s + 1) * k // planes)
+                            for s in range(planes)])
+            for s in range(planes):
+                check_parity(p[s], exp[s], k // planes, f"plane {s}")
+
+
+def test_tile_dispatch_with_m_and_ragged_edges(rt, bufs):
+    """tile_ir ABI (build_kernargs_m, src/t0/tile_ir.rs:3173) on M/N that are not
+    tile multiples, NN layout (B stored [K][N])."""
+    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(transpose=t0g.NN)
+    kern = rt.ensure_tile_kernel(cfg)
+    m, k, n = 200, 192, 136
+    a = o.make_bf16_suite(m * k, 1).reshape(m, k)
+    b = o.make_bf16_suite(k * n, 2).reshape(k, n)
+    ref = o.gemm("NN", a, b, m, n, k)
+    aa, ba = bufs.up(a), bufs.up(b)
+    y = bufs.up(np.full((m + 64, n), -9999.0, dtype=np.float32))
+    ka = t0g.build_kernargs_m(aa, ba, y, k, n, m, cfg)
+    grid = t0g.tile_compute_grid(cfg, m, n)
+    rt.dispatch(kern, grid, ka)
+    got = rt.read(y, (m + 64, n), np.float32)
+    check_parity(got[:m], ref, k, "tile ABI 200x192x136 NN")
+    assert np.all(got[m:] == -9999.0)
+
+
+def test_backward_helpers_with_host_transposes(rt, bufs):
+    """examples/test_gemm_backward.rs:130-287: dX via build_kernargs_backward_data on
+    W = WT^T, dW via build_kernargs_backward_weight on dY^T and X^T (host transposes)."""
+    m, k, n = 128, 256, 512
+    x = o.rand_bf16_xorshift(m * k, m * 100 + k)
+    w = o.rand_bf16_xorshift(n * k, n * 200 + k)      # WT [N,K]
+    dy = o.rand_bf16_xorshift(m * n, m * 300 + n)
+    cpu_dx = o.gemm("NN", dy, w, m, k, n)             # dX[i,j] = sum_p dY[i,p] W[p,j]
+    cpu_dw = o.gemm("TN", dy, x, n, k, m)             # dW[i,j] = sum_p dY[p,i] X[p,j]
+    w_t = o.transpose_bf16(w, n, k)                    # [K,N]
+    cfg = t0g.auto_select_backward_data(m, n, k)
+    kern = rt.ensure_gemm_kernel(cfg)
+    dya, wta = bufs.up(dy), bufs.up(w_t)
+    planes = max(cfg.split_k, 1)
+    dx = bufs.alloc(m * k * 4 * planes, fill=0)
+    ka = t0g.build_kernargs_backward_data(dya, wta, dx, m, n, k, cfg)
+    gx, gy = t0g.compute_grid_backward_data(cfg, m, k)
+    rt.dispatch(kern, [gx, gy, 1], ka)
+    check_parity(o.splitk_reduce(rt.read(dx, (planes, m, k), np.float32)), cpu_dx, n, "bwd data")
+    dy_t = o.transpose_bf16(dy, m, n)                  # [N,M]
+    x_t = o.transpose_bf16(x, m, k)                    # [K,M]
+    cfgw = t0g.auto_select_backward_weight(m, n, k)
+    kw = rt.ensure_gemm_kernel(cfgw)
+    dyt, xt = bufs.up(dy_t), bufs.up(x_t)
+    planes = max(cfgw.split_k, 1)
+    dw = bufs.alloc(n * k * 4 * planes, fill=0)
+    ka = t0g.build_kernargs_backward_weight(dyt, xt, dw, m, n, k, cfgw)
+    gx, gy = t0g.compute_grid_backward_weight(cfgw, n, k)
+    rt.dispatch(kw, [gx, gy, 1], ka)
+    check_parity(o.splitk_reduce(rt.read(dw, (planes, n, k), np.float32)), cpu_dw, m, "bwd weight")
+
+
+@pytest.mark.parametrize("epi", [t0g.EPI_BIAS_ADD, t0g.EPI_BIAS_ADD_RELU])
+@pytest.mark.parametrize("split_k", [0, 4])
+def test_bias_epilogues(rt, bufs, epi, split_k):
+    """gemm_gen EpilogueOp (src/t0/gemm_gen.rs:41-49): acc + bias[col], optional ReLU."""
+    m, k, n = 192, 512, 320
+    a = o.rand_bf16_xorshift(m * k, 5).reshape(m, k)
+    b = o.rand_bf16_xorshift(n * k, 6).reshape(n, k)
+    bias = (np.arange(n, dtype=np.float32) - n / 2) * 0.25
+    ref = o.gemm("NT", a, b, m, n, k) + bias[None, :]
+    if epi == t0g.EPI_BIAS_ADD_RELU:
+        ref = np.maximum(ref, 0.0)
+    bp = bufs.up(bias)
+    c = run_gemm(rt, bufs, "NT", a, b, m, n, k, epilogue=epi, bias=bp, split_k=split_k)
+    check_parity(c, ref, k, f"epilogue {epi} sk={split_k}")
+    if epi == t0g.EPI_BIAS_ADD_RELU:
+        assert c.min() >= 0.0
+
+
+def test_raw_kernel_load_and_dispatch(rt, bufs):
+    """GpuKernel::load path (src/kfd/mod.rs:2559): load a code object from bytes and
+    dispatch a symbol with raw kernargs (here this library's own NT kernel)."""
+    import struct
+    with open(os.path.join(os.path.dirname(t0g.LIB_PATH), "t0g_gemm_gfx950.hsaco"), "rb") as f:
+        blob = f.read()
+    kern = rt.load_kernel(blob, "t0g_gemm_128x128_k64_nt_f32", (256, 1, 1))
+    m, k, n = 256, 128, 384
+    a = o.rand_bf16_lcg(m * k, 9)
+    b = o.rand_bf16_lcg(n * k, 10)
+    aa, ba = bufs.up(a), bufs.up(b)
+    c = bufs.alloc(m * n * 4, fill=0)
+    tm, tn = m // 128, n // 128
+    # T0gGemmArgs: a b c bias c_split_stride | m n k lda ldb ldc k_per_split tiles_m tiles_n epilogue group_m flags
+    ka = struct.pack("<QQQQQ" + "I" * 12, aa, ba, c, 0, 0, m, n, k, k, k, n, k, tm, tn, 0, 8, 1)
+    rt.dispatch(kern, [tm * tn * 256, 1, 1], ka)
+    check_parity(rt.read(c, (m, n), np.float32), o.gemm("NT", a, b, m, n, k), k, "raw dispatch")
+
+
+def test_invalid_dispatch_is_rejected(rt, bufs):
+    cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+    kern = rt.ensure_gemm_kernel(cfg)
+    ka = bytearray(t0g.build_kernargs(1 << 20, 1 << 21, 1 << 22, 512, 64, 64, cfg))
+    ka[36:40] = b"\0\0\0\0"   # y_split_stride = 0 with split_k > 1
+    with pytest.raises(t0g.T0gError) as e:
+        rt.dispatch(kern, [256, 4, 1], bytes(ka))
+    assert e.value.code == t0g.ERR_INVALID_ARG
+    with pytest.raises(t0g.T0gError):
+        rt.dispatch(kern, [255, 4, 1], t0g.build_kernargs(1, 2, 3, 512, 64, 64, cfg))   # not a multiple of wg
+    with pytest.raises(t0g.T0gError):
+        rt.dispatch(kern, [256, 4, 1], b"\0" * 16)                                      # short kernargs
+    assert not rt.is_poisoned()
+
+
+def test_injected_failure_poisons_the_device():
+    """GpuRuntime poisons itself after a failed dispatch (src/ignis/gpu_context.rs:150-157)."""
+    r = t0g.GpuRuntime.new(0)
+    try:
+        m = n = k = 128
+        a = r.alloc(m * k * 2)
+        b = r.alloc(n * k * 2)
+        c = r.alloc(m * n * 4)
+        r.gemm(a, b, c, m, n, k)
+        r.wait_idle()
+        t0g.debug_fail_hip_call(2)   # hipSetDevice passes, the launch fails
+        with pytest.raises(t0g.T0gError) as e:
+            r.gemm(a, b, c, m, n, k)
+        assert e.value.code == t0g.ERR_HIP
+        assert r.is_poisoned()
+        with pytest.raises(t0g.T0gError) as e:
+            r.gemm(a, b, c, m, n, k)
+        assert e.value.code == t0g.ERR_POISONED
+    finally:
+        t0g.debug_fail_hip_call(0)
+        r.close()

@@ -1,0 +1,173 @@
+"""Host-side checks of the C ABI (no GPU): symbol table, GemmConfig mirror,
+selection, grids, kernarg byte layouts and the error paths.
+
+Byte layouts and grid formulas are the reference's (src/t0/gemm_gen.rs:286-309,
+402-456; src/t0/tile_ir.rs:3173-3202); the assertions follow its own unit tests
+(src/t0/gemm_gen.rs:548-584, 620-630; src/t0/tile_ir.rs:2875-2894)."""
+import ctypes
+import os
+import re
+import struct
+
+import pytest
+
+import t0g
+from conftest import ROOT
+
+
+def _declared_symbols():
+    with open(os.path.join(ROOT, "include", "t0g.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"T0G_API\s+[^;(]*?\b(t0g_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = _declared_symbols()
+    assert len(syms) >= 40
+    lib = t0g.library()
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_library_links_no_oracle():
+    with open(t0g.LIB_PATH, "rb") as f:
+        blob = f.read()
+    assert b"oracle_gemm" not in blob and b"liboracle" not in blob
+
+
+def test_version_and_last_error():
+    assert "gfx950" in t0g.version()
+    with pytest.raises(t0g.T0gError) as e:
+        t0g.GemmConfig.preset("tile_64x64_k16")   # an RDNA3 preset: no gfx950 kernel
+    assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG
+    assert "unknown preset" in t0g.last_error()
+
+
+@pytest.mark.parametrize("name,bm,bn", [("tile_256x256_k64", 256, 256), ("tile_128x128_k64", 128, 128),
+                                        ("tile_64x64_k64", 64, 64)])
+def test_presets_and_derived_fields(name, bm, bn):
+    c = t0g.GemmConfig.preset(name)
+    c.validate()
+    assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size) == (bm, bn, 64, 256)
+    assert c.n_waves() == 4                        # wave64
+    assert c.lds_total() == 2 * (bm + bn) * 64 * 2  # lds_total: 2 buffers x (X + WT) tiles
+    assert c.name() == f"t0_gemm_{bm}x{bn}_k64_ldsdb"
+    assert c.copy(split_k=4).name() == f"t0_gemm_{bm}x{bn}_k64_ldsdb_sk4"
+    assert c.copy(swap_grid=0).name().endswith("_mg")
+    assert c.copy(transpose=t0g.NN).name().endswith("_nn")
+    assert c.copy(epilogue=t0g.EPI_BIAS_ADD).name().endswith("_bias")
+    assert c.copy(epilogue=t0g.EPI_BIAS_ADD_RELU).name().endswith("_bias_relu")
+
+
+def test_invalid_configs_are_errors_not_panics():
+    c = t0g.GemmConfig.preset("tile_128x128_k64")
+    for bad in (dict(tile_m=96), dict(tile_k=16), dict(wg_size=128), dict(split_k=3), dict(split_k=128),
+                dict(n_col_passes=2), dict(double_buffer=0)):
+        with pytest.raises(t0g.T0gError) as e:
+            c.copy(**bad).validate()
+        assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG, bad
+
+
+def test_auto_select_reference_assertions():
+    # src/t0/gemm_gen.rs:548-573
+    c = t0g.auto_select(256, 256, 256)
+    assert 16 <= c.tile_m <= 256 and c.wg_size >= 32
+    c = t0g.auto_select(1024, 1024, 1024)
+    assert c.tile_m >= 64
+    c = t0g.auto_select(8192, 8192, 8192)
+    assert c.tile_m >= 64
+    c = t0g.auto_select(128, 4096, 4096)
+    assert 128 % c.tile_m == 0
+    for m, k, n in [(256, 256, 256), (4096, 4096, 4096), (8192, 8192, 8192), (128, 4096, 4096),
+                    (256, 32768, 256), (1024, 4096, 11008), (1024, 11008, 4096), (11008, 1024, 4096), (1, 1, 1)]:
+        t0g.auto_select(m, k, n).validate()
+
+
+def test_auto_select_table_for_256_cus():
+    big = t0g.auto_select(8192, 8192, 8192)
+    assert (big.tile_m, big.tile_n, big.split_k) == (256, 256, 0)
+    sq = t0g.auto_select(4096, 4096, 4096)
+    assert (sq.tile_m, sq.tile_n, sq.split_k) == (256, 256, 0)   # 256 tiles: one per CU
+    thin = t0g.auto_select(128, 4096, 4096)
+    tiles = (-(-128 // thin.tile_m)) * (-(-4096 // thin.tile_n)) * max(thin.split_k, 1)
+    assert tiles >= 128                                            # thin M is spread with split-K
+    deep = t0g.auto_select(256, 32768, 256)
+    assert deep.split_k >= 8                                       # 256x256 output, K=32768: split K
+    assert t0g.tile_auto_select(128, 256, 64, t0g.NN).transpose == t0g.NN
+
+
+def test_compute_grid_formulas():
+    c = t0g.GemmConfig.preset("tile_128x128_k64")
+    assert t0g.compute_grid(c, 1000, 300) == (3 * 256, 8)          # ceil(300/128)*wg, ceil(1000/128)
+    assert t0g.compute_grid(c.copy(swap_grid=0), 1000, 300) == (8 * 256, 3)
+    assert t0g.compute_grid_split_k(c, 256, 256, 4) == (2 * 256, 2 * 4)
+    with pytest.raises(t0g.T0gError):
+        t0g.compute_grid_split_k(c, 256, 256, 3)
+    assert t0g.compute_grid_auto(c.copy(split_k=8), 256, 512) == (4 * 256, 16)
+    assert t0g.compute_grid_auto(c, 256, 512) == (4 * 256, 2)
+    assert t0g.tile_compute_grid(c.copy(split_k=2), 129, 65) == [1 * 256, 2 * 2, 1]
+
+
+def test_build_kernargs_layout():
+    c = t0g.GemmConfig.preset("tile_64x64_k64")
+    ka = t0g.build_kernargs(0x1000, 0x2000, 0x3000, 64, 96, 128, c)
+    assert len(ka) == 40
+    assert struct.unpack("<QQQIIII", ka) == (0x1000, 0x2000, 0x3000, 64, 96, 0, 0)
+    ka = t0g.build_kernargs(0x1000, 0x2000, 0x3000, 512, 96, 128, c.copy(split_k=4))
+    assert struct.unpack("<QQQIIII", ka)[6] == 128 * 96 * 4          # y_split_stride = M*N*4
+    kb = t0g.build_kernargs_with_bias(0x1000, 0x2000, 0x3000, 64, 64, 128, c, 0x4000)
+    assert len(kb) == 48 and struct.unpack("<Q", kb[40:48])[0] == 0x4000   # gemm_gen.rs:620-630
+    km = t0g.build_kernargs_m(1, 2, 3, 64, 96, 77, c.copy(split_k=8))
+    assert len(km) == 44 and struct.unpack("<QQQIIIII", km) == (1, 2, 3, 64, 96, 3, 0, 77)
+
+
+def test_backward_helpers_argument_mapping():
+    m, n_orig, k_orig = 1024, 4096, 11008
+    cd = t0g.auto_select_backward_data(m, n_orig, k_orig)
+    assert cd.as_dict() == t0g.auto_select(m, n_orig, k_orig).as_dict()
+    cw = t0g.auto_select_backward_weight(m, n_orig, k_orig)
+    assert cw.as_dict() == t0g.auto_select(n_orig, m, k_orig).as_dict()
+    ka = t0g.build_kernargs_backward_data(10, 20, 30, m, n_orig, k_orig, cd)
+    assert struct.unpack("<QQQII", ka[:32]) == (10, 20, 30, n_orig, k_orig)     # K=N_orig, N=K_orig
+    kw = t0g.build_kernargs_backward_weight(10, 20, 30, m, n_orig, k_orig, cw)
+    assert struct.unpack("<QQQII", kw[:32]) == (10, 20, 30, m, k_orig)          # K=M, N=K_orig
+    assert t0g.compute_grid_backward_data(cd, m, k_orig) == t0g.compute_grid_auto(cd, m, k_orig)
+    assert t0g.compute_grid_backward_weight(cw, n_orig, k_orig) == t0g.compute_grid_auto(cw, n_orig, k_orig)
+
+
+def test_gemm_plan_selection_host_only():
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, transpose="NN", out_dtype=t0g.BF16)
+    assert t0g.gemm_kernel_name(d) == "t0g_gemm_256x256_k64_nn_bf16"
+    assert t0g.gemm_workspace_size(d) == 0
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 33, 50, 100)          # K % 8 != 0: element-wise loads
+    assert t0g.gemm_kernel_name(d).endswith("_u")
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 256, 256, 32768)
+    assert t0g.gemm_kernel_name(d).endswith("_nt_f32")
+    ws = t0g.gemm_workspace_size(d)
+    cfg = t0g.auto_select(256, 32768, 256)
+    assert ws == cfg.split_k * 256 * 256 * 4
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 64, 64, 64, split_k=4)
+    assert t0g.gemm_workspace_size(d) == 0        # K=64 is one tile: nothing to split
+    with pytest.raises(t0g.T0gError) as e:
+        t0g.gemm_kernel_name(t0g.gemm_desc(1, 2, 3, 64, 64, 64, ldc=10))
+    assert e.value.code == t0g.ERR_INVALID_ARG
+    with pytest.raises(t0g.T0gError):
+        t0g.gemm_kernel_name(t0g.gemm_desc(1, 2, 3, 64, 64, 64, epilogue=t0g.EPI_BIAS_ADD))   # no bias pointer
+
+
+def test_no_device_on_this_host_is_an_error():
+    if t0g.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(t0g.T0gError) as e:
+        t0g.GpuRuntime.new(0)
+    assert e.value.code == t0g.ERR_NO_DEVICE
+
+
+def test_injected_hip_failure_maps_to_error():
+    t0g.debug_fail_hip_call(1)
+    try:
+        with pytest.raises(t0g.T0gError) as e:
+            t0g.GpuRuntime.new(0)
+        assert e.value.code == t0g.ERR_HIP and "failed" in str(e.value)
+    finally:
+        t0g.debug_fail_hip_call(0)
