@@ -140,6 +140,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--only", metavar="LAYOUT:M:N:K",
+                    help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures the GEMM on one GPU only "
@@ -156,6 +158,19 @@ def main():
     stream = torch.cuda.Stream()
     rt.set_stream(stream.cuda_stream)
     torch.cuda.set_stream(stream)
+
+    if args.only:
+        lay, m, n, k = args.only.split(":")
+        m, n, k = int(m), int(n), int(k)
+        r = time_gemm(t0g, torch, rt, stream, m, n, k, lay.upper(), args.steps, args.warmup)
+        sec = r["event_ms_per_launch"] * 1e-3
+        print(json.dumps({"only": args.only, "kernel": r["kernel"], "us_per_launch": round(sec * 1e6, 2),
+                          "tflops": round(r["flop"] / sec / 1e12, 2),
+                          "frac_of_peak": round(r["flop"] / sec / 1e12 / PEAK_TFLOPS, 4),
+                          "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1)}), flush=True)
+        rt.set_stream(None)
+        rt.close()
+        return
 
     M = N = K = 4096
     keep = {}
@@ -196,6 +211,11 @@ def main():
         t8 = r8["flop"] / (r8["event_ms_per_launch"] * 1e-3) / 1e12
         extra["gemm_nn_8192^3"] = {"tflops": round(t8, 2), "frac_of_peak": round(t8 / PEAK_TFLOPS, 4),
                                    "ms_per_launch": round(r8["event_ms_per_launch"], 4), "kernel": r8["kernel"]}
+        log("[bench] 4096^3 NT bf16")
+        rnt = time_gemm(t0g, torch, rt, stream, 4096, 4096, 4096, "NT", args.steps, args.warmup, seed=6)
+        tnt = rnt["flop"] / (rnt["event_ms_per_launch"] * 1e-3) / 1e12
+        extra["gemm_nt_4096^3"] = {"tflops": round(tnt, 2), "frac_of_peak": round(tnt / PEAK_TFLOPS, 4),
+                                   "ms_per_launch": round(rnt["event_ms_per_launch"], 4), "kernel": rnt["kernel"]}
         for name, (m, n, k) in {"thin_128x4096x4096": (128, 4096, 4096),
                                 "splitk_256x256xK32768": (256, 256, 32768)}.items():
             log(f"[bench] {name}")

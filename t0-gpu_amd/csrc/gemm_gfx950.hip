@@ -28,6 +28,12 @@
 #include "t0g_kernel_args.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+// Global-memory pointer types: with an explicit address space the compiler
+// emits global_* instead of flat_* instructions (flat loads also count on
+// lgkmcnt, so every LDS wait would wait for them as well).
+typedef const __attribute__((address_space(1))) uint16_t gu16_t;
+typedef __attribute__((address_space(1))) float gf32_t;
+typedef __attribute__((address_space(1))) __bf16 gbf16_t;
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -80,8 +86,8 @@ struct KMajorTile {
         }
     }
 
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ base, uint32_t k0, uint32_t kend, bool full) {
-        const uint16_t* p = base + k0;
+    __device__ __forceinline__ void load(gu16_t* __restrict__ base, uint32_t k0, uint32_t kend, bool full) {
+        gu16_t* p = base + k0;
         if (full) {
 #pragma unroll
             for (int i = 0; i < kChunks; ++i) {
@@ -143,10 +149,10 @@ struct MNMajorTile {
         off = kb * 8 * ld + c;
     }
 
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ base, uint32_t k0, uint32_t kend,
+    __device__ __forceinline__ void load(gu16_t* __restrict__ base, uint32_t k0, uint32_t kend,
                                          bool full, uint32_t ld, uint32_t R) {
         if (!active) return;
-        const uint16_t* p = base + (size_t)k0 * ld + off;
+        gu16_t* p = base + (size_t)k0 * ld + off;
         const int krem = (int)kend - (int)(k0 + kb * 8);   // rows of this block inside K
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
@@ -188,7 +194,7 @@ template <int ROWS, int NT, bool ALIGNED>
 struct TileLoader<true, ROWS, NT, ALIGNED> {
     KMajorTile<ROWS, NT, ALIGNED> t;
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t R, uint32_t ld) { t.init(tid, row0, R, ld); }
-    __device__ __forceinline__ void load(const uint16_t* base, uint32_t k0, uint32_t kend, bool full, uint32_t, uint32_t) {
+    __device__ __forceinline__ void load(gu16_t* base, uint32_t k0, uint32_t kend, bool full, uint32_t, uint32_t) {
         t.load(base, k0, kend, full);
     }
     __device__ __forceinline__ void store(char* lds) const { t.store(lds); }
@@ -197,14 +203,53 @@ template <int ROWS, int NT, bool ALIGNED>
 struct TileLoader<false, ROWS, NT, ALIGNED> {
     MNMajorTile<ROWS, NT, ALIGNED> t;
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t R, uint32_t ld) { t.init(tid, row0, R, ld); }
-    __device__ __forceinline__ void load(const uint16_t* base, uint32_t k0, uint32_t kend, bool full, uint32_t ld, uint32_t R) {
+    __device__ __forceinline__ void load(gu16_t* base, uint32_t k0, uint32_t kend, bool full, uint32_t ld, uint32_t R) {
         t.load(base, k0, kend, full, ld, R);
     }
     __device__ __forceinline__ void store(char* lds) const { t.store(lds); }
 };
 
 // ---------------------------------------------------------------------------
-// The tile kernel body.
+// Epilogue: acc -> (+bias[col]) -> (ReLU) -> f32 or bf16 (round to nearest
+// even), masked to the M x N output.  32x32 MFMA result layout: lane
+// (l32 = lane % 32, g = lane / 32), register r holds row 8*(r/4) + 4*g + r%4,
+// column l32 of the 32x32 block.
+// ---------------------------------------------------------------------------
+template <int SM, int SN, bool OUT_BF16>
+__device__ __forceinline__ void store_tile(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
+                                           uint32_t col0, uint32_t l32, uint32_t g) {
+    const __attribute__((address_space(1))) float* bias =
+        reinterpret_cast<const __attribute__((address_space(1))) float*>(p.bias);
+    const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+#pragma unroll
+    for (int j = 0; j < SN; ++j) {
+        const uint32_t col = col0 + j * 32 + l32;
+        const bool col_ok = col < p.n;
+        float bv = 0.0f;
+        if (p.epilogue != 0 && col_ok) bv = bias[col];
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (col_ok && row < p.m) {
+                    float x = acc[i][j][r];
+                    if (p.epilogue != 0) x = x + bv;
+                    if (p.epilogue == 2) x = x > 0.0f ? x : 0.0f;
+                    const uint64_t idx = (uint64_t)row * p.ldc + col;
+                    if constexpr (OUT_BF16)
+                        reinterpret_cast<gbf16_t*>(cbase)[idx] = (__bf16)x;
+                    else
+                        reinterpret_cast<gf32_t*>(cbase)[idx] = x;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic tile body: element-wise loads for rows that are not 16-byte
+// aligned (K % 8 != 0 and the like); correctness path, not the fast path.
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, bool ALIGNED>
 __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
@@ -234,8 +279,8 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
     const int nkt = kend > kbeg ? (int)((kend - kbeg + kTileK - 1) / kTileK) : 0;
 
-    const uint16_t* __restrict__ A = reinterpret_cast<const uint16_t*>(p.a);
-    const uint16_t* __restrict__ B = reinterpret_cast<const uint16_t*>(p.b);
+    gu16_t* __restrict__ A = reinterpret_cast<gu16_t*>(p.a);
+    gu16_t* __restrict__ B = reinterpret_cast<gu16_t*>(p.b);
 
     TileLoader<A_K, BM, NT, ALIGNED> la;
     TileLoader<B_K, BN, NT, ALIGNED> lb;
@@ -298,35 +343,327 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
         }
     }
 
-    // --- epilogue: acc -> (+bias) -> (ReLU) -> f32 / bf16 (RNE) -----------------
-    // 32x32 MFMA result layout: lane (l32, g), register r holds
-    // row 8*(r/4) + 4*g + r%4, column l32 of the 32x32 block.
-    const float* __restrict__ bias = reinterpret_cast<const float*>(p.bias);
-    char* cbase = reinterpret_cast<char*>(p.c) + (size_t)blockIdx.y * p.c_split_stride;
+    store_tile<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l32, g);
+}
+
+// ---------------------------------------------------------------------------
+// Fast tile body (16-byte aligned operands).
+//
+// Operands reach LDS through range-checked buffer loads straight into LDS
+// (no VGPR staging).  The descriptor covers exactly the operand's extent, so
+// rows past M/N or K past the operand read as zero without a clamp, and a K
+// slice's tail is masked by sending the offset out of range.  The K loop is a
+// ring of NS LDS stages of 32 K each; per stage s (two MFMA steps of K = 16):
+//   issue the DMA of stage s + NS - 1 into the buffer stage s - 1 just freed
+//   step 0: read step-1 fragments of stage s          | MFMAs of step 0
+//   step 1: read step-0 fragments of stage s + 1      | MFMAs of step 1
+//   wait until the DMA of stage s + 2 has landed; barrier
+// Stage t's DMA thus has NS - 2 stages of MFMA work to arrive in, and the
+// fragment reads of the next stage are in flight before the barrier, so the
+// MFMA pipe does not drain at stage boundaries.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer descriptor word 3
+constexpr uint32_t kOob = 0x80000000u;    // offset past any descriptor range (operands < 2 GiB): loads return 0
+
+// Descriptor over [base + shift, base + bytes).  A shift at or past the end
+// gives an empty range (every load returns zero), never a wrapped one.
+__device__ __forceinline__ rsrc_t make_rsrc(uint64_t base, uint32_t bytes, uint64_t shift) {
+    const uint32_t rec = shift < bytes ? bytes - (uint32_t)shift : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base + shift), (short)0, (int)rec, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4_t bload16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Raw buffer descriptor words for [base + shift, base + bytes) (see make_rsrc).
+__device__ __forceinline__ u32x4_t rsrc_words(uint64_t base, uint32_t bytes, uint64_t shift) {
+    const uint32_t rec = shift < bytes ? bytes - (uint32_t)shift : 0u;
+    const uint64_t a = base + shift;
+    return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
+}
+
+// 16-byte buffer load straight into LDS: lane l's data goes to LDS address
+// m0 + 16 * l.  An SALU write of M0 needs one wait state before an LDS-DMA
+// instruction reads it, hence the s_nop.  Completion is tracked by vmcnt only
+// (callers wait with T0G_WAIT_VMCNT).
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voff, uint32_t lds_m0) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %1, 0 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(lds_m0)
+        : "memory", "m0");
+}
+
+// ---------------------------------------------------------------------------
+// LDS layouts of the fast path (K tile of 32):
+//   K-contiguous operand: one 64-byte row per M/N row; 16-byte chunk c of row r
+//     is stored at chunk c ^ fk(r).  32 (or 16) lanes reading one logical chunk
+//     of consecutive rows with ds_read_b128 touch distinct banks.
+//   M/N-contiguous operand: one row per k holding the tile's M/N extent; 32-byte
+//     granule q of row k is stored at granule q ^ fm(k).  The 4 rows x 2
+//     granules a half-wave of ds_read_b64_tr_b16 touches land in distinct banks.
+// Both operands are copied global -> LDS by the buffer unit (LDS DMA): one
+// wave instruction fills 1 KB, lane l writing the 16-byte slot l, so each lane
+// fetches the global piece that the swizzle places in its slot.  Rows and K
+// columns past the operand fall outside the descriptor range and read as zero.
+// ---------------------------------------------------------------------------
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+constexpr uint32_t kBK = 32;          // K elements per pipeline stage
+constexpr uint32_t kKRow = kBK * 2;   // bytes per K-contiguous LDS row
+
+__device__ __forceinline__ uint32_t fk(uint32_t row) { return ((row >> 1) ^ (row >> 3)) & 3u; }
+__device__ __forceinline__ uint32_t fm(uint32_t k, uint32_t granules) {
+    // {0, 2, 5, 7}[k % 4], reduced to the row's granule count
+    return ((0x7520u >> ((k & 3u) * 4)) & 0xFu) & (granules - 1);
+}
+
+template <bool K_MAJOR, int ROWS, int NT, int SUBS>
+struct DmaOperand;
+
+// Fragment reads are ordinary LDS loads: the compiler inserts their lgkmcnt
+// waits and the MFMA operand hazard padding.  (The LDS DMA is inline asm, so
+// the compiler's wait-count pass never sees DMA in flight and adds no vmcnt
+// drains before these reads.)
+__device__ __forceinline__ bf16x8_t lds_load_b128(uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>((uintptr_t)addr);
+}
+__device__ __forceinline__ void lds_load_tr16(uint32_t addr, short (&out)[4]) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(uintptr_t)addr);
+    out[0] = v[0];
+    out[1] = v[1];
+    out[2] = v[2];
+    out[3] = v[3];
+}
+
+// K-contiguous: LDS rows are M/N rows; one DMA instruction = 16 rows.
+template <int ROWS, int NT, int SUBS>
+struct DmaOperand<true, ROWS, NT, SUBS> {
+    static constexpr int kWaves = NT / 64;
+    static constexpr int kInstr = ROWS * kKRow / 1024 / kWaves;   // per wave per stage
+    static_assert(kInstr >= 1 && ROWS * kKRow % (1024 * kWaves) == 0, "tile too small for the workgroup");
+    static constexpr uint32_t kStageBytes = ROWS * kKRow;
+    uint32_t off[kInstr];    // byte offset of the lane's piece at k = 0
+    uint32_t kcol[kInstr];   // K column of the piece within the stage
+    uint32_t wave;
+    uint32_t frag[2];        // LDS byte offset (within a stage) of the lane's chunk, per 16-wide K step
+
+    __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow, uint32_t l32,
+                                         uint32_t g) {
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t lane = tid & 63u;
 #pragma unroll
-    for (int j = 0; j < SN; ++j) {
-        const uint32_t col = n0 + wn * WTN + j * 32 + l32;
-        const bool col_ok = col < p.n;
-        float bv = 0.0f;
-        if (p.epilogue != 0 && col_ok) bv = bias[col];
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t q = i * kWaves + wave;
+            const uint32_t r = 16 * q + (lane >> 2);
+            const uint32_t c = (lane & 3u) ^ fk(r);
+            kcol[i] = c * 8;
+            off[i] = ((row0 + r) * ld + c * 8) * 2;
+        }
+        // Row wrow + 32*sub + l32: fk depends on row bits 1..4 only, so the
+        // sub-tile term is a plain offset (32 rows = 2048 bytes).
+        const uint32_t row = wrow + l32;
+        frag[0] = row * kKRow + (((0u + g) ^ fk(row)) << 4);
+        frag[1] = row * kKRow + (((2u + g) ^ fk(row)) << 4);
+    }
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t, uint32_t k0,
+                                          uint32_t kend) const {
+        const u32x4_t r = rsrc_words(base, bytes, (uint64_t)k0 * 2);
 #pragma unroll
-        for (int i = 0; i < SM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (col_ok && row < p.m) {
-                    float x = acc[i][j][r];
-                    if (p.epilogue != 0) x = x + bv;
-                    if (p.epilogue == 2) x = x > 0.0f ? x : 0.0f;
-                    const size_t idx = (size_t)row * p.ldc + col;
-                    if constexpr (OUT_BF16)
-                        reinterpret_cast<__bf16*>(cbase)[idx] = (__bf16)x;
-                    else
-                        reinterpret_cast<float*>(cbase)[idx] = x;
-                }
-            }
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t voff = k0 + kcol[i] < kend ? off[i] : kOob;
+            dma16(r, voff, lds + (i * kWaves + wave) * 1024);
         }
     }
+    // Fragments of the SUBS sub-tiles (32 rows x 8 K values each) for K step kk
+    // of the stage at LDS address `stage`.
+    template <int KK>
+    __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
+        const uint32_t a = stage + frag[KK];
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) f[sub] = lds_load_b128(a + sub * 32 * kKRow);
+    }
+};
+
+// M/N-contiguous: LDS rows are k rows of ROWS elements.
+template <int ROWS, int NT, int SUBS>
+struct DmaOperand<false, ROWS, NT, SUBS> {
+    static constexpr int kWaves = NT / 64;
+    static constexpr uint32_t kRowB = ROWS * 2;
+    static constexpr uint32_t kGranules = ROWS / 16;
+    static constexpr uint32_t kStageBytes = kBK * kRowB;
+    static constexpr int kInstr = kStageBytes / 1024 / kWaves;
+    static_assert(kInstr >= 1 && kStageBytes % (1024 * kWaves) == 0, "tile too small for the workgroup");
+    static_assert(kGranules >= 4, "at least 4 granules per row");
+    uint32_t off[kInstr];
+    uint32_t krow[kInstr];
+    uint32_t wave;
+    uint32_t frag[SUBS];   // LDS byte offset (within a stage) of the lane's piece, K step 0, half 0
+
+    __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow, uint32_t l32,
+                                         uint32_t g) {
+        (void)l32;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t lane = tid & 63u;
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t pos = (i * kWaves + wave) * 1024 + lane * 16;   // byte in the stage
+            const uint32_t k = pos / kRowB;
+            const uint32_t slot = (pos % kRowB) / 16;
+            const uint32_t lg = (slot >> 1) ^ fm(k, kGranules);             // logical granule
+            krow[i] = k;
+            off[i] = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2;
+        }
+        // ds_read_b64_tr_b16: in each 16-lane group, lane 4r+q points at k row
+        // (base + r), columns colbase + 4q .. 4q+3; lane i then receives the 4
+        // k values of column colbase + i.  The row is k = 16*kk + 8*g + 4*h + r;
+        // fm depends on k % 4 = r only, so K step and half are plain offsets.
+        const uint32_t r = (lane >> 2) & 3u, q = lane & 3u, gp = (lane >> 4) & 1u;
+        const uint32_t k0 = 8 * g + r, f = fm(r, kGranules), gr = (wrow >> 4) + gp;
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) frag[sub] = k0 * kRowB + q * 8 + (((gr + 2 * sub) ^ f) << 5);
+    }
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
+                                          uint32_t kend) const {
+        const u32x4_t r = rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t voff = k0 + krow[i] < kend ? off[i] : kOob;
+            dma16(r, voff, lds + (i * kWaves + wave) * 1024);
+        }
+    }
+    template <int KK>
+    __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
+        constexpr int O0 = KK * 16 * kRowB, O1 = (KK * 16 + 4) * kRowB;
+#pragma unroll
+        for (int sub = 0; sub < SUBS; ++sub) {
+            short v[8];
+            short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
+            short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
+            lds_load_tr16(stage + frag[sub] + O0, lo);
+            lds_load_tr16(stage + frag[sub] + O1, hi);
+            typedef short v8s __attribute__((ext_vector_type(8)));
+            const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+            f[sub] = __builtin_bit_cast(bf16x8_t, w);
+        }
+    }
+};
+
+template <int SM, int SN>
+__device__ __forceinline__ void mfma_step(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM],
+                                          const bf16x8_t (&fb)[SN]) {
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+}
+
+// s_waitcnt with only vmcnt = n (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+#define T0G_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
+// Workgroup barrier without __syncthreads()'s release fence: the fence would
+// wait for every LDS DMA in flight (vmcnt(0)), draining the prefetch ring.
+// Callers retire exactly the DMA they need with T0G_WAIT_VMCNT first; the
+// asm memory clobbers keep the compiler from moving LDS accesses across it.
+// LDS reads still in flight at the barrier target the next stage's buffer,
+// which nobody overwrites before the following barrier, so no lgkmcnt wait.
+__device__ __forceinline__ void barrier_no_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, int NS>
+__device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int SM = WTM / 32, SN = WTN / 32;
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
+    static_assert(NS >= 4, "the pipeline needs at least 4 stages");
+    using OpA = DmaOperand<A_K, BM, NT, SM>;
+    using OpB = DmaOperand<B_K, BN, NT, SN>;
+    constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
+    constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
+    __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
+
+    const uint32_t tid = threadIdx.x;
+    uint32_t bid = blockIdx.x;
+    const uint32_t nblk = p.tiles_m * p.tiles_n;
+    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    const uint32_t gm = p.group_m;
+    const uint32_t per_group = gm * p.tiles_n;
+    const uint32_t group = bid / per_group;
+    const uint32_t first_m = group * gm;
+    const uint32_t gsz = min(p.tiles_m - first_m, gm);
+    const uint32_t in_group = bid - group * per_group;
+    const uint32_t m0 = (first_m + in_group % gsz) * BM;
+    const uint32_t n0 = (in_group / gsz) * BN;
+
+    const uint32_t kbeg = blockIdx.y * p.k_per_split;
+    const uint32_t kend = min(p.k, kbeg + p.k_per_split);
+    const int nst = kend > kbeg ? (int)((kend - kbeg + kBK - 1) / kBK) : 0;
+
+    const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+    const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const uint32_t l32 = lane & 31u, g = lane >> 5;
+    OpA la;
+    OpB lb;
+    la.init(tid, m0, p.lda, wm * WTM, l32, g);
+    lb.init(tid, n0, p.ldb, wn * WTN, l32, g);
+
+    f32x16_t acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = f32x16_t{};
+
+    if (nst > 0) {
+        bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
+        const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+        // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) {
+            la.issue(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * kBK, kend);
+            lb.issue(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * kBK, kend);
+        }
+        T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
+        barrier_no_fence();
+        la.template read<0>(lds0, fa0);
+        lb.template read<0>(lds0 + A_BYTES, fb0);
+
+        uint32_t cur = 0;                 // byte offset of stage s's buffer
+        uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
+        for (int s = 0; s < nst; ++s) {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * kBK;
+            la.issue(lds0 + fill, p.a, a_bytes, p.lda, kf, kend);
+            lb.issue(lds0 + fill + A_BYTES, p.b, b_bytes, p.ldb, kf, kend);
+            // K step 0 of stage s; read step 1
+            la.template read<1>(lds0 + cur, fa1);
+            lb.template read<1>(lds0 + cur + A_BYTES, fb1);
+            mfma_step<SM, SN>(acc, fa0, fb0);
+            // K step 1 of stage s; read step 0 of stage s+1 (landed before the last barrier)
+            la.template read<0>(lds0 + nxt, fa0);
+            lb.template read<0>(lds0 + nxt + A_BYTES, fb0);
+            mfma_step<SM, SN>(acc, fa1, fb1);
+            T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
+            barrier_no_fence();
+            fill = cur;
+            cur = nxt;
+        }
+    }
+    store_tile<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l32, g);
 }
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the
@@ -365,10 +702,18 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 #define T0G_WPE_256x256 1, 1
 #define T0G_WPE_128x128 1, 2
 #define T0G_WPE_64x64 1, 4
+// LDS ring depth of the fast path: 5 x 32 KB = 160 KB for 256x256 (one
+// workgroup per CU), 4 stages for the tiles that share a CU.
+#define T0G_NS_256x256 5
+#define T0G_NS_128x128 4
+#define T0G_NS_64x64 4
 #define T0G_GEMM(NAME, BM, BN, WM, WN, AK, BKM, OBF, AL)                                       \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                   \
         __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmArgs p) {          \
-        t0g::gemm_tile<BM, BN, WM, WN, AK, BKM, OBF, AL>(p);                                     \
+        if constexpr (AL)                                                                        \
+            t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_NS_##BM##x##BN>(p);            \
+        else                                                                                     \
+            t0g::gemm_tile<BM, BN, WM, WN, AK, BKM, OBF, AL>(p);                                 \
     }
 
 #define T0G_GEMM_LAYOUTS(PFX, BM, BN, WM, WN, OUTN, OBF, SFX, AL)          \

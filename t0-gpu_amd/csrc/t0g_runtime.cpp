@@ -175,9 +175,14 @@ struct GemmPlan {
     std::string symbol;
 };
 
+// The fast kernels need 16-byte aligned rows and operands under 2 GiB (their
+// buffer descriptors use 0x80000000 as the always-out-of-range offset).
 static bool operands_aligned(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
                              uint32_t t) {
     if ((a & 15) || (b & 15) || (lda & 7) || (ldb & 7)) return false;
+    const uint64_t a_elems = a_k_major(t) ? (uint64_t)m * lda : (uint64_t)k * lda;
+    const uint64_t b_elems = b_k_major(t) ? (uint64_t)n * ldb : (uint64_t)k * ldb;
+    if (a_elems >= (1ull << 30) || b_elems >= (1ull << 30)) return false;
     if (a_k_major(t) ? (k & 7) != 0 : ((m & 7) != 0 || m < 8)) return false;
     if (b_k_major(t) ? (k & 7) != 0 : ((n & 7) != 0 || n < 8)) return false;
     return true;

@@ -1,0 +1,156 @@
+"""Host-side model of the fast kernels' LDS layouts (no GPU).
+
+The gfx950 fast path copies operands into LDS with buffer-to-LDS DMA (lane l of
+a wave instruction writes 16-byte slot l of a 1 KB block) under an XOR
+swizzle, and reads MFMA fragments back with ds_read_b128 (K-contiguous
+operands) or two ds_read_b64_tr_b16 (M/N-contiguous operands).  This test
+replays that address arithmetic on a labelled tile and checks that every
+lane's fragment holds exactly the (row, k) elements the 32x32x16 MFMA
+expects: lane (l32, g) of K step kk needs k = 16*kk + 8*g + e, e = 0..7, of
+row (or column) l32 of its 32-wide sub-tile.
+
+ds_read_b64_tr_b16 semantics (measured on gfx950 with an in-bounds LDS probe):
+within each 16-lane group, lane i receives element i % 4 of the 8-byte pieces
+addressed by lanes 4*r + i // 4, r = 0..3.
+"""
+import numpy as np
+import pytest
+
+BK = 32
+
+
+# ---- the kernel's swizzles and address formulas (gemm_gfx950.hip) ----------
+def fk(row):
+    return ((row >> 1) ^ (row >> 3)) & 3
+
+
+def fm(k, granules):
+    return ((0x7520 >> ((k & 3) * 4)) & 0xF) & (granules - 1)
+
+
+def dma_kmajor(rows, waves):
+    """LDS byte -> (row, kcol) for the K-contiguous stage written by DMA."""
+    lds = {}
+    instr = rows * 64 // 1024 // waves
+    for wave in range(waves):
+        for i in range(instr):
+            q = i * waves + wave
+            for lane in range(64):
+                r = 16 * q + (lane >> 2)
+                c = (lane & 3) ^ fk(r)
+                for e in range(8):
+                    lds[q * 1024 + lane * 16 + 2 * e] = (r, c * 8 + e)
+    return lds
+
+
+def dma_mnmajor(rows, waves):
+    """LDS byte -> (row, kcol) for the M/N-contiguous stage written by DMA."""
+    lds = {}
+    row_bytes = rows * 2
+    granules = rows // 16
+    instr = BK * row_bytes // 1024 // waves
+    for wave in range(waves):
+        for i in range(instr):
+            base = (i * waves + wave) * 1024
+            for lane in range(64):
+                pos = base + lane * 16
+                k = pos // row_bytes
+                slot = (pos % row_bytes) // 16
+                lg = (slot >> 1) ^ fm(k, granules)
+                for e in range(8):
+                    lds[pos + 2 * e] = (lg * 16 + (slot & 1) * 8 + e, k)
+    return lds
+
+
+def frag_kmajor(lds, wrow, sub, kk):
+    out = {}
+    for lane in range(64):
+        l32, g = lane & 31, lane >> 5
+        row = wrow + l32
+        ch = ((2 * kk + g) ^ fk(row)) << 4
+        addr = row * 64 + sub * 32 * 64 + ch
+        out[lane] = [lds[addr + 2 * e] for e in range(8)]
+    return out
+
+
+def frag_mnmajor(lds, rows, wrow, sub, kk):
+    """Two ds_read_b64_tr_b16 per fragment, addresses as in the kernel."""
+    row_bytes = rows * 2
+    granules = rows // 16
+    addr = {}
+    for h in range(2):
+        for lane in range(64):
+            r, q, gp, g = (lane >> 2) & 3, lane & 3, (lane >> 4) & 1, lane >> 5
+            k = kk * 16 + 8 * g + 4 * h + r
+            f = fm(k, granules)
+            granule = (wrow >> 4) + 2 * sub + gp
+            addr[(h, lane)] = k * row_bytes + ((granule ^ f) << 5) + q * 8
+    out = {}
+    for lane in range(64):
+        grp, i = lane // 16, lane % 16
+        vals = []
+        for h in range(2):
+            for r in range(4):
+                src = 16 * grp + 4 * r + i // 4
+                vals.append(lds[addr[(h, src)] + 2 * (i % 4)])
+        out[lane] = vals
+    return out
+
+
+def expected(wrow, sub, kk):
+    return {lane: [(wrow + sub * 32 + (lane & 31), 16 * kk + 8 * (lane >> 5) + e) for e in range(8)]
+            for lane in range(64)}
+
+
+@pytest.mark.parametrize("rows", [64, 128, 256])
+def test_kmajor_dma_and_fragments(rows):
+    lds = dma_kmajor(rows, 4)
+    assert len(lds) == rows * 32                      # every element written once
+    for wrow in range(0, rows, rows // 2 if rows >= 64 else 32):
+        for sub in range(min(4, (rows // 2) // 32)):
+            for kk in range(2):
+                assert frag_kmajor(lds, wrow, sub, kk) == expected(wrow, sub, kk)
+
+
+@pytest.mark.parametrize("rows", [64, 128, 256])
+def test_mnmajor_dma_and_transposed_fragments(rows):
+    lds = dma_mnmajor(rows, 4)
+    assert len(lds) == rows * 32
+    wave_rows = rows // 2
+    for wrow in (0, wave_rows):
+        for sub in range(wave_rows // 32):
+            for kk in range(2):
+                assert frag_mnmajor(lds, rows, wrow, sub, kk) == expected(wrow, sub, kk)
+
+
+def _banks(addrs, width):
+    """Max accesses to one 4-byte bank among `addrs` (each a (byte, size) pair) per `width`-byte cycle."""
+    hits = {}
+    for a, size in addrs:
+        for b in range(a, a + size, 4):
+            bank = (b // 4) % (width // 4)
+            hits.setdefault(bank, set()).add(b // width)
+    return max(len(v) for v in hits.values())
+
+
+@pytest.mark.parametrize("rows", [128, 256])
+def test_fragment_reads_are_bank_conflict_free(rows):
+    # ds_read_b128, K-contiguous: 16-lane phases over 256 bytes of banks
+    for lane0 in range(0, 64, 16):
+        for kk in range(2):
+            addrs = []
+            for lane in range(lane0, lane0 + 16):
+                row = (lane & 31)
+                addrs.append((row * 64 + (((2 * kk + (lane >> 5)) ^ fk(row)) << 4), 16))
+            assert _banks(addrs, 256) == 1
+    # ds_read_b64_tr_b16, M/N-contiguous: 32-lane phases over 256 bytes of banks
+    row_bytes, granules = rows * 2, rows // 16
+    for half in range(2):
+        for sub in range(2):
+            for kk in range(2):
+                addrs = []
+                for lane in range(32 * half, 32 * half + 32):
+                    r, q, gp, g = (lane >> 2) & 3, lane & 3, (lane >> 4) & 1, lane >> 5
+                    k = kk * 16 + 8 * g + r
+                    addrs.append((k * row_bytes + (((2 * sub + gp) ^ fm(k, granules)) << 5) + q * 8, 8))
+                assert _banks(addrs, 256) == 1
