@@ -474,22 +474,28 @@ struct DmaOperand<true, ROWS, NT, SUBS> {
         frag[0] = row * kKRow + (((0u + g) ^ fk(row)) << 4);
         frag[1] = row * kKRow + (((2u + g) ^ fk(row)) << 4);
     }
-    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t, uint32_t k0,
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
-        const u32x4_t r = rsrc_words(base, bytes, (uint64_t)k0 * 2);
+        const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) {
-            const uint32_t voff = k0 + kcol[i] < kend ? off[i] : kOob;
-            dma16(r, voff, lds + (i * kWaves + wave) * 1024);
-        }
+        for (int i = 0; i < kInstr; ++i) issue_one(i, r, lds, k0, kend);
+    }
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t, uint32_t k0) const {
+        return rsrc_words(base, bytes, (uint64_t)k0 * 2);
+    }
+    __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
+        dma16(r, k0 + kcol[i] < kend ? off[i] : kOob, lds + (i * kWaves + wave) * 1024);
     }
     // Fragments of the SUBS sub-tiles (32 rows x 8 K values each) for K step kk
     // of the stage at LDS address `stage`.
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
-        const uint32_t a = stage + frag[KK];
 #pragma unroll
-        for (int sub = 0; sub < SUBS; ++sub) f[sub] = lds_load_b128(a + sub * 32 * kKRow);
+        for (int sub = 0; sub < SUBS; ++sub) f[sub] = read_one<KK>(stage, sub);
+    }
+    template <int KK>
+    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
+        return lds_load_b128(stage + frag[KK] + sub * 32 * kKRow);
     }
 };
 
@@ -533,27 +539,32 @@ struct DmaOperand<false, ROWS, NT, SUBS> {
     }
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
-        const u32x4_t r = rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+        const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) {
-            const uint32_t voff = k0 + krow[i] < kend ? off[i] : kOob;
-            dma16(r, voff, lds + (i * kWaves + wave) * 1024);
-        }
+        for (int i = 0; i < kInstr; ++i) issue_one(i, r, lds, k0, kend);
+    }
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
+        return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+    }
+    __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
+        dma16(r, k0 + krow[i] < kend ? off[i] : kOob, lds + (i * kWaves + wave) * 1024);
     }
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
-        constexpr int O0 = KK * 16 * kRowB, O1 = (KK * 16 + 4) * kRowB;
 #pragma unroll
-        for (int sub = 0; sub < SUBS; ++sub) {
-            short v[8];
-            short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
-            short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
-            lds_load_tr16(stage + frag[sub] + O0, lo);
-            lds_load_tr16(stage + frag[sub] + O1, hi);
-            typedef short v8s __attribute__((ext_vector_type(8)));
-            const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
-            f[sub] = __builtin_bit_cast(bf16x8_t, w);
-        }
+        for (int sub = 0; sub < SUBS; ++sub) f[sub] = read_one<KK>(stage, sub);
+    }
+    template <int KK>
+    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
+        constexpr int O0 = KK * 16 * kRowB, O1 = (KK * 16 + 4) * kRowB;
+        short v[8];
+        short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
+        short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
+        lds_load_tr16(stage + frag[sub] + O0, lo);
+        lds_load_tr16(stage + frag[sub] + O1, hi);
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+        return __builtin_bit_cast(bf16x8_t, w);
     }
 };
 
@@ -579,6 +590,46 @@ __device__ __forceinline__ void barrier_no_fence() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// One 16-wide K step: SM rows of SN MFMAs on (fa, fb); interleaved with the
+// LDS reads of the next step's fragments into (na, nb) and with this step's
+// share of the DMA instructions (the first half of a stage's DMA in step 0,
+// the second half in step 1).  sched_barrier pins the row order.
+template <int STEP, int SM, int SN, int NDMA, class OpA, class OpB>
+__device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
+                                          bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
+                                          uint32_t stage_cur, uint32_t stage_next, uint32_t fill, u32x4_t ra,
+                                          u32x4_t rb, uint32_t kf, uint32_t kend) {
+    constexpr int NEXT_KK = STEP == 0 ? 1 : 0;
+    const uint32_t rd = STEP == 0 ? stage_cur : stage_next;
+    constexpr int kHalf = (NDMA + 1) / 2;
+    constexpr int kFirst = STEP * kHalf;
+    constexpr int kCount = (STEP == 0 ? kHalf : NDMA - kHalf);
+    constexpr int kPerRow = (kCount + SM - 1) / SM;
+    (void)stage_cur;
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        na[i] = la.template read_one<NEXT_KK>(rd, i);
+        if (i < SN) nb[i] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, i);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int d = 0; d < kPerRow; ++d) {
+            constexpr int dummy = 0;
+            (void)dummy;
+            const int q = kFirst + i * kPerRow + d;
+            if (q < kFirst + kCount) {
+                if (q < OpA::kInstr)
+                    la.issue_one(q, ra, fill, kf, kend);
+                else
+                    lb.issue_one(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = SM; j < SN; ++j) nb[j] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, j);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, int NS>
@@ -647,16 +698,16 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
         for (int s = 0; s < nst; ++s) {
             const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
             const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * kBK;
-            la.issue(lds0 + fill, p.a, a_bytes, p.lda, kf, kend);
-            lb.issue(lds0 + fill + A_BYTES, p.b, b_bytes, p.ldb, kf, kend);
-            // K step 0 of stage s; read step 1
-            la.template read<1>(lds0 + cur, fa1);
-            lb.template read<1>(lds0 + cur + A_BYTES, fb1);
-            mfma_step<SM, SN>(acc, fa0, fb0);
-            // K step 1 of stage s; read step 0 of stage s+1 (landed before the last barrier)
-            la.template read<0>(lds0 + nxt, fa0);
-            lb.template read<0>(lds0 + nxt + A_BYTES, fb0);
-            mfma_step<SM, SN>(acc, fa1, fb1);
+            const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+            const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+            // K step 0 of stage s (reads: step 1 of stage s), then K step 1
+            // (reads: step 0 of stage s+1, landed before the last barrier).
+            // Each row of MFMAs is followed by part of the DMA of stage
+            // s + NS - 1, so MFMAs stay queued while a DMA instruction issues.
+            mfma_rows<0, SM, SN, kVmemPerStage>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + cur,
+                                                lds0 + fill, ra, rb, kf, kend);
+            mfma_rows<1, SM, SN, kVmemPerStage>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt,
+                                                lds0 + fill, ra, rb, kf, kend);
             T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
             barrier_no_fence();
             fill = cur;
