@@ -141,7 +141,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
-                    help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs")
+                    help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
+                         "COPY:MiB instead times a plain device-to-device copy of that size, the "
+                         "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures the GEMM on one GPU only "
@@ -158,6 +160,26 @@ def main():
     stream = torch.cuda.Stream()
     rt.set_stream(stream.cuda_stream)
     torch.cuda.set_stream(stream)
+
+    if args.only and args.only.upper().startswith("COPY:"):
+        nbytes = int(float(args.only.split(":")[1]) * (1 << 20)) // 16 * 16
+        src = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / args.steps
+        print(json.dumps({"only": args.only, "bytes_read": nbytes, "bytes_written": nbytes,
+                          "us_per_copy": round(sec * 1e6, 2), "gbs": round(2 * nbytes / sec / 1e9, 1)}), flush=True)
+        rt.set_stream(None)
+        rt.close()
+        return
 
     if args.only:
         lay, m, n, k = args.only.split(":")
