@@ -39,6 +39,8 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 namespace t0g {
 
+constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer descriptor word 3
+
 constexpr int kTileK = 64;       // bf16 elements of K per tile
 constexpr int kRowBytes = 128;   // one LDS row holds the tile's K slice of one M/N row
 
@@ -215,27 +217,46 @@ struct TileLoader<false, ROWS, NT, ALIGNED> {
 // (l32 = lane % 32, g = lane / 32), register r holds row 8*(r/4) + 4*g + r%4,
 // column l32 of the 32x32 block.
 // ---------------------------------------------------------------------------
+// The bias values are fetched up front with range-checked buffer loads (columns
+// past N read as 0) and retired with one explicit wait, so the per-element
+// stores below carry no memory waits and stream out back to back.
+template <int SN>
+__device__ __forceinline__ void load_bias_cols(const T0gGemmArgs& p, uint32_t col0, uint32_t l32, float (&bv)[SN]) {
+#pragma unroll
+    for (int j = 0; j < SN; ++j) bv[j] = 0.0f;
+    if (p.epilogue != 0) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+            bv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + j * 32 + l32) * 4u, 0, 0));
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    }
+}
+
+__device__ __forceinline__ float apply_epilogue(float x, float bv, uint32_t epi) {
+    if (epi != 0) x = x + bv;
+    if (epi == 2) x = x > 0.0f ? x : 0.0f;
+    return x;
+}
+
 template <int SM, int SN, bool OUT_BF16>
 __device__ __forceinline__ void store_tile(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
                                            uint32_t col0, uint32_t l32, uint32_t g) {
-    const __attribute__((address_space(1))) float* bias =
-        reinterpret_cast<const __attribute__((address_space(1))) float*>(p.bias);
     const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+    float bv[SN];
+    load_bias_cols<SN>(p, col0, l32, bv);
 #pragma unroll
     for (int j = 0; j < SN; ++j) {
         const uint32_t col = col0 + j * 32 + l32;
         const bool col_ok = col < p.n;
-        float bv = 0.0f;
-        if (p.epilogue != 0 && col_ok) bv = bias[col];
 #pragma unroll
         for (int i = 0; i < SM; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (col_ok && row < p.m) {
-                    float x = acc[i][j][r];
-                    if (p.epilogue != 0) x = x + bv;
-                    if (p.epilogue == 2) x = x > 0.0f ? x : 0.0f;
+                    const float x = apply_epilogue(acc[i][j][r], bv[j], p.epilogue);
                     const uint64_t idx = (uint64_t)row * p.ldc + col;
                     if constexpr (OUT_BF16)
                         reinterpret_cast<gbf16_t*>(cbase)[idx] = (__bf16)x;
@@ -244,6 +265,101 @@ __device__ __forceinline__ void store_tile(const T0gGemmArgs& p, const f32x16_t 
                 }
             }
         }
+    }
+}
+
+// Epilogue of a tile that lies wholly inside C (and C rows are 16-byte
+// aligned): each wave stages its WTM x WTN result through its own LDS region,
+// 32 rows at a time, as f32 rows padded to WTN + 8 words -- the two lane
+// halves of a 32x32 result sit 4 rows apart and so land in opposite halves of
+// the 64 banks -- and writes whole rows back with 16-byte stores (4 f32 or
+// 8 bf16 per lane), so every store instruction covers complete 128-byte lines.
+template <int SN>
+struct VecEpilogue {
+    static constexpr int kWTN = SN * 32;
+    static constexpr uint32_t kStride = (kWTN + 8) * 4;   // bytes per staged row
+    static constexpr uint32_t kWaveBytes = 32 * kStride;   // LDS per wave
+};
+
+template <int SM, int SN, bool OUT_BF16>
+__device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
+                                               uint32_t col0, uint32_t lane, uint32_t lds, bool vec) {
+    typedef VecEpilogue<SN> E;
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) float lds_f32;
+    typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
+    constexpr int kCols = OUT_BF16 ? 8 : 4;              // columns per lane and store
+    constexpr int kLanesPerRow = E::kWTN / kCols;
+    constexpr int kRowsPerPass = 64 / kLanesPerRow;
+    static_assert(kLanesPerRow <= 64 && 64 % kLanesPerRow == 0, "row must map onto whole lanes");
+    const uint32_t l32 = lane & 31u, g = lane >> 5;
+    const uint32_t rl = lane / kLanesPerRow, cl = (lane % kLanesPerRow) * kCols;
+    float bv[kCols];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
+    if (p.epilogue != 0) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
+#pragma unroll
+        for (int c = 0; c < kCols; ++c)
+            bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + cl + c) * 4u, 0, 0));
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    }
+    const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+    const uint32_t esize = OUT_BF16 ? 2u : 4u;
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = 8 * (r >> 2) + 4 * g + (r & 3);
+                *reinterpret_cast<lds_f32*>((uintptr_t)(lds + row * E::kStride + (j * 32 + l32) * 4)) = acc[i][j][r];
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int pass = 0; pass < 32 / kRowsPerPass; ++pass) {
+            const uint32_t rr = pass * kRowsPerPass + rl;
+            float v[kCols];
+#pragma unroll
+            for (int c = 0; c < kCols; c += 4) {
+                const f32x4_t q = *reinterpret_cast<const lds_f32x4*>((uintptr_t)(lds + rr * E::kStride + (cl + c) * 4));
+                v[c] = q[0];
+                v[c + 1] = q[1];
+                v[c + 2] = q[2];
+                v[c + 3] = q[3];
+            }
+#pragma unroll
+            for (int c = 0; c < kCols; ++c) v[c] = apply_epilogue(v[c], bv[c], p.epilogue);
+            const uint32_t grow = row0 + i * 32 + rr, gcol = col0 + cl;
+            const uint64_t addr = cbase + ((uint64_t)grow * p.ldc + gcol) * esize;
+            if (vec) {
+                u32x4_t w;
+                if constexpr (OUT_BF16) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const __bf16 lo = (__bf16)v[2 * c], hi = (__bf16)v[2 * c + 1];
+                        w[c] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) w[c] = __builtin_bit_cast(uint32_t, v[c]);
+                }
+                *reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr) = w;
+            } else if (grow < p.m) {
+#pragma unroll
+                for (int c = 0; c < kCols; ++c) {
+                    if (gcol + c < p.n) {
+                        if constexpr (OUT_BF16)
+                            reinterpret_cast<gbf16_t*>((uintptr_t)addr)[c] = (__bf16)v[c];
+                        else
+                            reinterpret_cast<gf32_t*>((uintptr_t)addr)[c] = v[c];
+                    }
+                }
+            }
+        }
+        asm volatile("" ::: "memory");
     }
 }
 
@@ -363,7 +479,6 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
 // MFMA pipe does not drain at stage boundaries.
 // ---------------------------------------------------------------------------
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer descriptor word 3
 constexpr uint32_t kOob = 0x80000000u;    // offset past any descriptor range (operands < 2 GiB): loads return 0
 
 // Descriptor over [base + shift, base + bytes).  A shift at or past the end
@@ -608,16 +723,25 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
     constexpr int kCount = (STEP == 0 ? kHalf : NDMA - kHalf);
     constexpr int kPerRow = (kCount + SM - 1) / SM;
     (void)stage_cur;
+    // Fragment reads of the next step, B first (the next step's first row
+    // needs all of B but only A[0]), spread evenly over the rows so each has
+    // at least two rows of MFMAs to land.
+    constexpr int kReads = SM + SN;
+    constexpr int kReadsPerRow = (kReads + SM - 1) / SM;
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
-        na[i] = la.template read_one<NEXT_KK>(rd, i);
-        if (i < SN) nb[i] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, i);
+#pragma unroll
+        for (int d = 0; d < kReadsPerRow; ++d) {
+            const int q = i * kReadsPerRow + d;
+            if (q < SN)
+                nb[q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, q);
+            else if (q < kReads)
+                na[q - SN] = la.template read_one<NEXT_KK>(rd, q - SN);
+        }
 #pragma unroll
         for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 #pragma unroll
         for (int d = 0; d < kPerRow; ++d) {
-            constexpr int dummy = 0;
-            (void)dummy;
             const int q = kFirst + i * kPerRow + d;
             if (q < kFirst + kCount) {
                 if (q < OpA::kInstr)
@@ -628,8 +752,6 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int j = SM; j < SN; ++j) nb[j] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, j);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, int NS>
@@ -714,7 +836,14 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
             cur = nxt;
         }
     }
-    store_tile<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l32, g);
+    // Epilogue through LDS: 16-byte row stores for tiles wholly inside an
+    // aligned C, per-element masked stores otherwise.
+    static_assert(4 * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
+    T0G_WAIT_VMCNT(0);    // LDS DMA still in flight (stages past K) has landed
+    barrier_no_fence();   // and every wave is done with the ring
+    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+    store_tile_vec<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                     lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec);
 }
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the

@@ -20,7 +20,7 @@ typedef struct T0gGemmArgs {
     uint32_t tiles_n;        /* output tiles along N covered by the grid          */
     uint32_t epilogue;       /* 0 store, 1 +bias[col], 2 +bias[col] then ReLU     */
     uint32_t group_m;        /* tile-order group height (L2 reuse), >= 1          */
-    uint32_t flags;          /* bit0: remap block ids across the 8 XCDs           */
+    uint32_t flags;          /* T0G_FLAG_* bits                                   */
 } T0gGemmArgs;
 
 typedef struct T0gReduceArgs {
@@ -35,6 +35,7 @@ typedef struct T0gReduceArgs {
     uint32_t pad_;
 } T0gReduceArgs;
 
-#define T0G_FLAG_XCD_REMAP 1u
+#define T0G_FLAG_XCD_REMAP 1u   /* remap block ids so each XCD owns a contiguous tile range */
+#define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
 
 #endif

@@ -282,6 +282,9 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
         args.epilogue = o.epilogue;
         args.bias = o.bias;
     }
+    const uint64_t esize = reduce || !p.out_bf16 ? 4 : 2;
+    if ((args.c & 15) == 0 && ((uint64_t)args.ldc * esize) % 16 == 0 && args.c_split_stride % 16 == 0)
+        args.flags |= T0G_FLAG_C_VEC;
     rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.tile->wg, &args, sizeof args);
     if (rc || !reduce) return rc;
 
