@@ -514,10 +514,13 @@ __device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voff, uint32_t lds_
 }
 
 // ---------------------------------------------------------------------------
-// LDS layouts of the fast path (K tile of 32):
-//   K-contiguous operand: one 64-byte row per M/N row; 16-byte chunk c of row r
-//     is stored at chunk c ^ fk(r).  32 (or 16) lanes reading one logical chunk
-//     of consecutive rows with ds_read_b128 touch distinct banks.
+// LDS layouts of the fast path (one pipeline stage holds BK = 32 or 64 K
+// values of both operand tiles):
+//   K-contiguous operand: one BK*2-byte row per M/N row; 16-byte chunk c of
+//     row r is stored at chunk c ^ fk<BK>(r).  The 16 lanes of a ds_read_b128
+//     phase read one logical chunk of 16 consecutive rows and touch distinct
+//     banks.  One DMA instruction fills 1 KB = 16 rows (BK 32) or 8 whole
+//     128-byte rows (BK 64, so every request is a full cache line).
 //   M/N-contiguous operand: one row per k holding the tile's M/N extent; 32-byte
 //     granule q of row k is stored at granule q ^ fm(k).  The 4 rows x 2
 //     granules a half-wave of ds_read_b64_tr_b16 touches land in distinct banks.
@@ -531,16 +534,25 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-constexpr uint32_t kBK = 32;          // K elements per pipeline stage
-constexpr uint32_t kKRow = kBK * 2;   // bytes per K-contiguous LDS row
-
-__device__ __forceinline__ uint32_t fk(uint32_t row) { return ((row >> 1) ^ (row >> 3)) & 3u; }
+// Chunk swizzle of a K-contiguous row.  A 16-byte chunk's bank group (of 16)
+// is (row * chunks_per_row + chunk) % 16.  BK 32 (4 chunks, 64 B rows): rows
+// r, r+4, r+8, r+12 get four different values, so 16 consecutive rows reading
+// one logical chunk cover all 16 groups.  BK 64 (8 chunks, 128 B rows): the 8
+// rows of one parity among 16 consecutive rows get 8 different values.
+// Neither depends on row bits >= 5, so 32-row sub-tiles are plain offsets.
+template <uint32_t BK>
+__device__ __forceinline__ uint32_t fk(uint32_t row) {
+    if constexpr (BK == 32)
+        return ((row >> 1) ^ (row >> 3)) & 3u;
+    else
+        return (row >> 1) & 7u;
+}
 __device__ __forceinline__ uint32_t fm(uint32_t k, uint32_t granules) {
     // {0, 2, 5, 7}[k % 4], reduced to the row's granule count
     return ((0x7520u >> ((k & 3u) * 4)) & 0xFu) & (granules - 1);
 }
 
-template <bool K_MAJOR, int ROWS, int NT, int SUBS>
+template <bool K_MAJOR, int ROWS, int NT, int SUBS, uint32_t BK>
 struct DmaOperand;
 
 // Fragment reads are ordinary LDS loads: the compiler inserts their lgkmcnt
@@ -559,17 +571,21 @@ __device__ __forceinline__ void lds_load_tr16(uint32_t addr, short (&out)[4]) {
     out[3] = v[3];
 }
 
-// K-contiguous: LDS rows are M/N rows; one DMA instruction = 16 rows.
-template <int ROWS, int NT, int SUBS>
-struct DmaOperand<true, ROWS, NT, SUBS> {
+// K-contiguous: LDS rows are M/N rows of BK*2 bytes.
+template <int ROWS, int NT, int SUBS, uint32_t BK>
+struct DmaOperand<true, ROWS, NT, SUBS, BK> {
     static constexpr int kWaves = NT / 64;
+    static constexpr uint32_t kKRow = BK * 2;                      // bytes per LDS row
+    static constexpr uint32_t kChunks = BK / 8;                    // 16-byte chunks per row
+    static constexpr uint32_t kRowsPerInstr = 64 / kChunks;
     static constexpr int kInstr = ROWS * kKRow / 1024 / kWaves;   // per wave per stage
+    static constexpr int kSteps = BK / 16;
     static_assert(kInstr >= 1 && ROWS * kKRow % (1024 * kWaves) == 0, "tile too small for the workgroup");
     static constexpr uint32_t kStageBytes = ROWS * kKRow;
     uint32_t off[kInstr];    // byte offset of the lane's piece at k = 0
     uint32_t kcol[kInstr];   // K column of the piece within the stage
     uint32_t wave;
-    uint32_t frag[2];        // LDS byte offset (within a stage) of the lane's chunk, per 16-wide K step
+    uint32_t frag[kSteps];   // LDS byte offset (within a stage) of the lane's chunk, per 16-wide K step
 
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow, uint32_t l32,
                                          uint32_t g) {
@@ -578,16 +594,14 @@ struct DmaOperand<true, ROWS, NT, SUBS> {
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) {
             const uint32_t q = i * kWaves + wave;
-            const uint32_t r = 16 * q + (lane >> 2);
-            const uint32_t c = (lane & 3u) ^ fk(r);
+            const uint32_t r = kRowsPerInstr * q + lane / kChunks;
+            const uint32_t c = (lane % kChunks) ^ fk<BK>(r);
             kcol[i] = c * 8;
             off[i] = ((row0 + r) * ld + c * 8) * 2;
         }
-        // Row wrow + 32*sub + l32: fk depends on row bits 1..4 only, so the
-        // sub-tile term is a plain offset (32 rows = 2048 bytes).
         const uint32_t row = wrow + l32;
-        frag[0] = row * kKRow + (((0u + g) ^ fk(row)) << 4);
-        frag[1] = row * kKRow + (((2u + g) ^ fk(row)) << 4);
+#pragma unroll
+        for (int kk = 0; kk < kSteps; ++kk) frag[kk] = row * kKRow + (((2u * kk + g) ^ fk<BK>(row)) << 4);
     }
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
@@ -601,26 +615,26 @@ struct DmaOperand<true, ROWS, NT, SUBS> {
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
         dma16(r, k0 + kcol[i] < kend ? off[i] : kOob, lds + (i * kWaves + wave) * 1024);
     }
-    // Fragments of the SUBS sub-tiles (32 rows x 8 K values each) for K step kk
-    // of the stage at LDS address `stage`.
+    // Fragment of sub-tile `sub` (32 rows x 8 K values) for K step KK of the
+    // stage at LDS address `stage`.
+    template <int KK>
+    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
+        return lds_load_b128(stage + frag[KK] + sub * 32 * kKRow);
+    }
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
 #pragma unroll
         for (int sub = 0; sub < SUBS; ++sub) f[sub] = read_one<KK>(stage, sub);
     }
-    template <int KK>
-    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
-        return lds_load_b128(stage + frag[KK] + sub * 32 * kKRow);
-    }
 };
 
 // M/N-contiguous: LDS rows are k rows of ROWS elements.
-template <int ROWS, int NT, int SUBS>
-struct DmaOperand<false, ROWS, NT, SUBS> {
+template <int ROWS, int NT, int SUBS, uint32_t BK>
+struct DmaOperand<false, ROWS, NT, SUBS, BK> {
     static constexpr int kWaves = NT / 64;
     static constexpr uint32_t kRowB = ROWS * 2;
     static constexpr uint32_t kGranules = ROWS / 16;
-    static constexpr uint32_t kStageBytes = kBK * kRowB;
+    static constexpr uint32_t kStageBytes = BK * kRowB;
     static constexpr int kInstr = kStageBytes / 1024 / kWaves;
     static_assert(kInstr >= 1 && kStageBytes % (1024 * kWaves) == 0, "tile too small for the workgroup");
     static_assert(kGranules >= 4, "at least 4 granules per row");
@@ -707,25 +721,22 @@ __device__ __forceinline__ void barrier_no_fence() {
     asm volatile("" ::: "memory");
 }
 
-// One 16-wide K step: SM rows of SN MFMAs on (fa, fb); interleaved with the
-// LDS reads of the next step's fragments into (na, nb) and with this step's
-// share of the DMA instructions (the first half of a stage's DMA in step 0,
-// the second half in step 1).  sched_barrier pins the row order.
-template <int STEP, int SM, int SN, int NDMA, class OpA, class OpB>
+// One 16-wide K step (STEP of NSTEPS in a stage): SM rows of SN MFMAs on
+// (fa, fb), interleaved with the LDS reads of the next step's fragments into
+// (na, nb) -- from stage `cur`, or from `nxt` after the stage's last step --
+// and with DMA instructions [DFIRST, DFIRST + DCOUNT) of the stage being
+// filled.  sched_barrier pins the row order, so MFMAs stay queued while a DMA
+// instruction issues.
+template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
                                           bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
-                                          uint32_t stage_cur, uint32_t stage_next, uint32_t fill, u32x4_t ra,
-                                          u32x4_t rb, uint32_t kf, uint32_t kend) {
-    constexpr int NEXT_KK = STEP == 0 ? 1 : 0;
-    const uint32_t rd = STEP == 0 ? stage_cur : stage_next;
-    constexpr int kHalf = (NDMA + 1) / 2;
-    constexpr int kFirst = STEP * kHalf;
-    constexpr int kCount = (STEP == 0 ? kHalf : NDMA - kHalf);
-    constexpr int kPerRow = (kCount + SM - 1) / SM;
-    (void)stage_cur;
+                                          uint32_t cur, uint32_t nxt, uint32_t fill, u32x4_t ra, u32x4_t rb,
+                                          uint32_t kf, uint32_t kend) {
+    constexpr int NEXT_KK = (STEP + 1) % NSTEPS;
+    const uint32_t rd = STEP + 1 < NSTEPS ? cur : nxt;
+    constexpr int kPerRow = (DCOUNT + SM - 1) / SM;
     // Fragment reads of the next step, B first (the next step's first row
-    // needs all of B but only A[0]), spread evenly over the rows so each has
-    // at least two rows of MFMAs to land.
+    // needs all of B but only A[0]), spread evenly over the rows.
     constexpr int kReads = SM + SN;
     constexpr int kReadsPerRow = (kReads + SM - 1) / SM;
 #pragma unroll
@@ -742,8 +753,8 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
         for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 #pragma unroll
         for (int d = 0; d < kPerRow; ++d) {
-            const int q = kFirst + i * kPerRow + d;
-            if (q < kFirst + kCount) {
+            const int q = DFIRST + i * kPerRow + d;
+            if (q < DFIRST + DCOUNT) {
                 if (q < OpA::kInstr)
                     la.issue_one(q, ra, fill, kf, kend);
                 else
@@ -754,17 +765,22 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
     }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, int NS>
+// Fast path.  BK 32 with a ring of NS >= 4 stages (DMA NS-1 stages ahead,
+// one barrier per stage), or BK 64 with NS = 2 (double buffer: the DMA of
+// stage s+1 is issued during the first half of stage s and retired, with one
+// barrier, before the stage's last K step reads stage s+1's first fragments).
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS>
 __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 32, SN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-    static_assert(NS >= 4, "the pipeline needs at least 4 stages");
-    using OpA = DmaOperand<A_K, BM, NT, SM>;
-    using OpB = DmaOperand<B_K, BN, NT, SN>;
+    static_assert((BK == 32 && NS >= 4) || (BK == 64 && NS == 2), "unsupported pipeline shape");
+    using OpA = DmaOperand<A_K, BM, NT, SM, BK>;
+    using OpB = DmaOperand<B_K, BN, NT, SN, BK>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
     constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
+    constexpr int kSteps = BK / 16;
     __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
     const uint32_t tid = threadIdx.x;
@@ -782,7 +798,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
 
     const uint32_t kbeg = blockIdx.y * p.k_per_split;
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
-    const int nst = kend > kbeg ? (int)((kend - kbeg + kBK - 1) / kBK) : 0;
+    const int nst = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
 
     const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
     const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
@@ -804,38 +820,70 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     if (nst > 0) {
         bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
         const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-        // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
+        if constexpr (BK == 32) {
+            // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
 #pragma unroll
-        for (int s = 0; s < NS - 1; ++s) {
-            la.issue(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * kBK, kend);
-            lb.issue(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * kBK, kend);
-        }
-        T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
-        barrier_no_fence();
-        la.template read<0>(lds0, fa0);
-        lb.template read<0>(lds0 + A_BYTES, fb0);
-
-        uint32_t cur = 0;                 // byte offset of stage s's buffer
-        uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
-        for (int s = 0; s < nst; ++s) {
-            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
-            const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * kBK;
-            const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
-            const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-            // K step 0 of stage s (reads: step 1 of stage s), then K step 1
-            // (reads: step 0 of stage s+1, landed before the last barrier).
-            // Each row of MFMAs is followed by part of the DMA of stage
-            // s + NS - 1, so MFMAs stay queued while a DMA instruction issues.
-            mfma_rows<0, SM, SN, kVmemPerStage>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + cur,
-                                                lds0 + fill, ra, rb, kf, kend);
-            mfma_rows<1, SM, SN, kVmemPerStage>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt,
-                                                lds0 + fill, ra, rb, kf, kend);
-            T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
+            for (int s = 0; s < NS - 1; ++s) {
+                la.issue(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * BK, kend);
+                lb.issue(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * BK, kend);
+            }
+            T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
             barrier_no_fence();
-            fill = cur;
-            cur = nxt;
+            la.template read<0>(lds0, fa0);
+            lb.template read<0>(lds0 + A_BYTES, fb0);
+
+            constexpr int kHalf = (kVmemPerStage + 1) / 2;
+            uint32_t cur = 0;                 // byte offset of stage s's buffer
+            uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
+            for (int s = 0; s < nst; ++s) {
+                const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+                const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * BK;
+                const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+                const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+                // K step 0 of stage s (reads: step 1 of stage s), then K step 1
+                // (reads: step 0 of stage s+1, landed before the last barrier).
+                mfma_rows<0, 2, 0, kHalf>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill,
+                                          ra, rb, kf, kend);
+                mfma_rows<1, 2, kHalf, kVmemPerStage - kHalf>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                               lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+                T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
+                barrier_no_fence();
+                fill = cur;
+                cur = nxt;
+            }
+        } else {
+            static_assert(kSteps == 4, "BK 64 has four K steps");
+            la.issue(lds0, p.a, a_bytes, p.lda, kbeg, kend);
+            lb.issue(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
+            T0G_WAIT_VMCNT(0);
+            barrier_no_fence();
+            la.template read<0>(lds0, fa0);
+            lb.template read<0>(lds0 + A_BYTES, fb0);
+
+            constexpr int kHalf = (kVmemPerStage + 1) / 2;
+            uint32_t cur = 0;
+            for (int s = 0; s < nst; ++s) {
+                const uint32_t nxt = cur ^ STAGE;   // the other buffer, freed by the previous barrier
+                const uint32_t kf = kbeg + (uint32_t)(s + 1) * BK;
+                const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+                const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+                mfma_rows<0, 4, 0, kHalf>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
+                                          ra, rb, kf, kend);
+                mfma_rows<1, 4, kHalf, kVmemPerStage - kHalf>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                               lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
+                mfma_rows<2, 4, 0, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
+                                      kf, kend);
+                // Stage s+1 has landed (all waves) and every wave's reads of
+                // stage s are complete, so the next iteration may refill it.
+                __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+                barrier_no_fence();
+                mfma_rows<3, 4, 0, 0>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
+                                      kf, kend);
+                cur = nxt;
+            }
         }
     }
+
     // Epilogue through LDS: 16-byte row stores for tiles wholly inside an
     // aligned C, per-element masked stores otherwise.
     static_assert(4 * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
@@ -882,16 +930,17 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 #define T0G_WPE_256x256 1, 1
 #define T0G_WPE_128x128 1, 2
 #define T0G_WPE_64x64 1, 4
-// LDS ring depth of the fast path: 5 x 32 KB = 160 KB for 256x256 (one
-// workgroup per CU), 4 stages for the tiles that share a CU.
-#define T0G_NS_256x256 5
-#define T0G_NS_128x128 4
-#define T0G_NS_64x64 4
+// Fast-path pipeline (K values per stage, stages): 256x256 double-buffers
+// 2 x 64 KB stages of BK 64 (whole 128-byte rows per request, one workgroup per
+// CU); the smaller tiles, which share a CU, keep a 4-deep ring of BK 32 stages.
+#define T0G_PIPE_256x256 64, 2
+#define T0G_PIPE_128x128 32, 4
+#define T0G_PIPE_64x64 32, 4
 #define T0G_GEMM(NAME, BM, BN, WM, WN, AK, BKM, OBF, AL)                                       \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                   \
         __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmArgs p) {          \
         if constexpr (AL)                                                                        \
-            t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_NS_##BM##x##BN>(p);            \
+            t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_##BM##x##BN>(p);            \
         else                                                                                     \
             t0g::gemm_tile<BM, BN, WM, WN, AK, BKM, OBF, AL>(p);                                 \
     }

@@ -16,39 +16,37 @@ addressed by lanes 4*r + i // 4, r = 0..3.
 import numpy as np
 import pytest
 
-BK = 32
-
-
 # ---- the kernel's swizzles and address formulas (gemm_gfx950.hip) ----------
-def fk(row):
-    return ((row >> 1) ^ (row >> 3)) & 3
+def fk(row, bk=32):
+    return ((row >> 1) ^ (row >> 3)) & 3 if bk == 32 else (row >> 1) & 7
 
 
 def fm(k, granules):
     return ((0x7520 >> ((k & 3) * 4)) & 0xF) & (granules - 1)
 
 
-def dma_kmajor(rows, waves):
+def dma_kmajor(rows, waves, bk=32):
     """LDS byte -> (row, kcol) for the K-contiguous stage written by DMA."""
     lds = {}
-    instr = rows * 64 // 1024 // waves
+    chunks = bk // 8
+    instr = rows * bk * 2 // 1024 // waves
     for wave in range(waves):
         for i in range(instr):
             q = i * waves + wave
             for lane in range(64):
-                r = 16 * q + (lane >> 2)
-                c = (lane & 3) ^ fk(r)
+                r = (64 // chunks) * q + lane // chunks
+                c = (lane % chunks) ^ fk(r, bk)
                 for e in range(8):
                     lds[q * 1024 + lane * 16 + 2 * e] = (r, c * 8 + e)
     return lds
 
 
-def dma_mnmajor(rows, waves):
+def dma_mnmajor(rows, waves, bk=32):
     """LDS byte -> (row, kcol) for the M/N-contiguous stage written by DMA."""
     lds = {}
     row_bytes = rows * 2
     granules = rows // 16
-    instr = BK * row_bytes // 1024 // waves
+    instr = bk * row_bytes // 1024 // waves
     for wave in range(waves):
         for i in range(instr):
             base = (i * waves + wave) * 1024
@@ -62,13 +60,13 @@ def dma_mnmajor(rows, waves):
     return lds
 
 
-def frag_kmajor(lds, wrow, sub, kk):
+def frag_kmajor(lds, wrow, sub, kk, bk=32):
     out = {}
     for lane in range(64):
         l32, g = lane & 31, lane >> 5
         row = wrow + l32
-        ch = ((2 * kk + g) ^ fk(row)) << 4
-        addr = row * 64 + sub * 32 * 64 + ch
+        ch = ((2 * kk + g) ^ fk(row, bk)) << 4
+        addr = row * bk * 2 + sub * 32 * bk * 2 + ch
         out[lane] = [lds[addr + 2 * e] for e in range(8)]
     return out
 
@@ -102,24 +100,28 @@ def expected(wrow, sub, kk):
             for lane in range(64)}
 
 
-@pytest.mark.parametrize("rows", [64, 128, 256])
-def test_kmajor_dma_and_fragments(rows):
-    lds = dma_kmajor(rows, 4)
-    assert len(lds) == rows * 32                      # every element written once
+# (rows, K per stage): 256x256 stages hold 64 K values, the smaller tiles 32
+SHAPES = [(64, 32), (128, 32), (256, 32), (256, 64)]
+
+
+@pytest.mark.parametrize("rows,bk", SHAPES)
+def test_kmajor_dma_and_fragments(rows, bk):
+    lds = dma_kmajor(rows, 4, bk)
+    assert len(lds) == rows * bk                      # every element written once
     for wrow in range(0, rows, rows // 2 if rows >= 64 else 32):
         for sub in range(min(4, (rows // 2) // 32)):
-            for kk in range(2):
-                assert frag_kmajor(lds, wrow, sub, kk) == expected(wrow, sub, kk)
+            for kk in range(bk // 16):
+                assert frag_kmajor(lds, wrow, sub, kk, bk) == expected(wrow, sub, kk)
 
 
-@pytest.mark.parametrize("rows", [64, 128, 256])
-def test_mnmajor_dma_and_transposed_fragments(rows):
-    lds = dma_mnmajor(rows, 4)
-    assert len(lds) == rows * 32
+@pytest.mark.parametrize("rows,bk", SHAPES)
+def test_mnmajor_dma_and_transposed_fragments(rows, bk):
+    lds = dma_mnmajor(rows, 4, bk)
+    assert len(lds) == rows * bk
     wave_rows = rows // 2
     for wrow in (0, wave_rows):
         for sub in range(wave_rows // 32):
-            for kk in range(2):
+            for kk in range(bk // 16):
                 assert frag_mnmajor(lds, rows, wrow, sub, kk) == expected(wrow, sub, kk)
 
 
@@ -133,21 +135,21 @@ def _banks(addrs, width):
     return max(len(v) for v in hits.values())
 
 
-@pytest.mark.parametrize("rows", [128, 256])
-def test_fragment_reads_are_bank_conflict_free(rows):
+@pytest.mark.parametrize("rows,bk", [(128, 32), (256, 32), (256, 64)])
+def test_fragment_reads_are_bank_conflict_free(rows, bk):
     # ds_read_b128, K-contiguous: 16-lane phases over 256 bytes of banks
     for lane0 in range(0, 64, 16):
-        for kk in range(2):
+        for kk in range(bk // 16):
             addrs = []
             for lane in range(lane0, lane0 + 16):
                 row = (lane & 31)
-                addrs.append((row * 64 + (((2 * kk + (lane >> 5)) ^ fk(row)) << 4), 16))
+                addrs.append((row * bk * 2 + (((2 * kk + (lane >> 5)) ^ fk(row, bk)) << 4), 16))
             assert _banks(addrs, 256) == 1
     # ds_read_b64_tr_b16, M/N-contiguous: 32-lane phases over 256 bytes of banks
     row_bytes, granules = rows * 2, rows // 16
     for half in range(2):
         for sub in range(2):
-            for kk in range(2):
+            for kk in range(bk // 16):
                 addrs = []
                 for lane in range(32 * half, 32 * half + 32):
                     r, q, gp, g = (lane >> 2) & 3, lane & 3, (lane >> 4) & 1, lane >> 5
