@@ -603,17 +603,23 @@ struct DmaOperand<true, ROWS, NT, SUBS, BK> {
 #pragma unroll
         for (int kk = 0; kk < kSteps; ++kk) frag[kk] = row * kKRow + (((2u * kk + g) ^ fk<BK>(row)) << 4);
     }
+    template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
         const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) issue_one(i, r, lds, k0, kend);
+        for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
     __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t, uint32_t k0) const {
         return rsrc_words(base, bytes, (uint64_t)k0 * 2);
     }
+    // CHECK: mask pieces at or past kend (a stage holding the K tail).  Without
+    // it, pieces past kend read whatever follows in memory (or zero past the
+    // descriptor range): fine for stages that are never consumed.
+    template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
-        dma16(r, k0 + kcol[i] < kend ? off[i] : kOob, lds + (i * kWaves + wave) * 1024);
+        const uint32_t voff = CHECK ? (k0 + kcol[i] < kend ? off[i] : kOob) : off[i];
+        dma16(r, voff, lds + (i * kWaves + wave) * 1024);
     }
     // Fragment of sub-tile `sub` (32 rows x 8 K values) for K step KK of the
     // stage at LDS address `stage`.
@@ -666,17 +672,23 @@ struct DmaOperand<false, ROWS, NT, SUBS, BK> {
 #pragma unroll
         for (int sub = 0; sub < SUBS; ++sub) frag[sub] = k0 * kRowB + q * 8 + (((gr + 2 * sub) ^ f) << 5);
     }
+    template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
         const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) issue_one(i, r, lds, k0, kend);
+        for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
     __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
         return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
     }
+    // CHECK: mask pieces at or past kend (a stage holding the K tail).  Without
+    // it, pieces past kend read whatever follows in memory (or zero past the
+    // descriptor range): fine for stages that are never consumed.
+    template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
-        dma16(r, k0 + krow[i] < kend ? off[i] : kOob, lds + (i * kWaves + wave) * 1024);
+        const uint32_t voff = CHECK ? (k0 + krow[i] < kend ? off[i] : kOob) : off[i];
+        dma16(r, voff, lds + (i * kWaves + wave) * 1024);
     }
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
@@ -727,7 +739,7 @@ __device__ __forceinline__ void barrier_no_fence() {
 // and with DMA instructions [DFIRST, DFIRST + DCOUNT) of the stage being
 // filled.  sched_barrier pins the row order, so MFMAs stay queued while a DMA
 // instruction issues.
-template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, int SM, int SN, class OpA, class OpB>
+template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, bool CHECK, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
                                           bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
                                           uint32_t cur, uint32_t nxt, uint32_t fill, u32x4_t ra, u32x4_t rb,
@@ -756,19 +768,91 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
             const int q = DFIRST + i * kPerRow + d;
             if (q < DFIRST + DCOUNT) {
                 if (q < OpA::kInstr)
-                    la.issue_one(q, ra, fill, kf, kend);
+                    la.template issue_one<CHECK>(q, ra, fill, kf, kend);
                 else
-                    lb.issue_one(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+                    lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// Fast path.  BK 32 with a ring of NS >= 4 stages (DMA NS-1 stages ahead,
-// one barrier per stage), or BK 64 with NS = 2 (double buffer: the DMA of
-// stage s+1 is issued during the first half of stage s and retired, with one
-// barrier, before the stage's last K step reads stage s+1's first fragments).
+// The K loop of the fast path.  BK 32: ring of NS >= 4 stages, DMA NS-1
+// stages ahead, one barrier per stage.  BK 64: NS = 2 (double buffer): the DMA
+// of stage s+1 is issued during the first half of stage s and retired, with one
+// barrier, before the stage's last K step reads stage s+1's first fragments.
+template <bool CHECK, uint32_t BK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN,
+          class OpA, class OpB>
+__device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& la, const OpB& lb, const T0gGemmArgs& p,
+                                           uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg, uint32_t kend, int nst,
+                                           uint32_t lds0) {
+    bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
+    if constexpr (BK == 32) {
+        // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) {
+            la.template issue<CHECK>(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * BK, kend);
+            lb.template issue<CHECK>(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * BK, kend);
+        }
+        T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
+        barrier_no_fence();
+        la.template read<0>(lds0, fa0);
+        lb.template read<0>(lds0 + A_BYTES, fb0);
+
+        constexpr int kHalf = (kVmemPerStage + 1) / 2;
+        uint32_t cur = 0;                 // byte offset of stage s's buffer
+        uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
+        for (int s = 0; s < nst; ++s) {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * BK;
+            const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+            const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+            // K step 0 of stage s (reads: step 1 of stage s), then K step 1
+            // (reads: step 0 of stage s+1, landed before the last barrier).
+            mfma_rows<0, 2, 0, kHalf, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill,
+                                      ra, rb, kf, kend);
+            mfma_rows<1, 2, kHalf, kVmemPerStage - kHalf, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                           lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+            T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
+            barrier_no_fence();
+            fill = cur;
+            cur = nxt;
+        }
+    } else {
+        static_assert(BK == 64 && NS == 2, "BK 64 double-buffers");
+        la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
+        lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
+        T0G_WAIT_VMCNT(0);
+        barrier_no_fence();
+        la.template read<0>(lds0, fa0);
+        lb.template read<0>(lds0 + A_BYTES, fb0);
+
+        constexpr int kHalf = (kVmemPerStage + 1) / 2;
+        uint32_t cur = 0;
+        for (int s = 0; s < nst; ++s) {
+            const uint32_t nxt = cur ^ STAGE;   // the other buffer, freed by the previous barrier
+            const uint32_t kf = kbeg + (uint32_t)(s + 1) * BK;
+            const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+            const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+            mfma_rows<0, 4, 0, kHalf, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
+                                      ra, rb, kf, kend);
+            mfma_rows<1, 4, kHalf, kVmemPerStage - kHalf, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                           lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
+            mfma_rows<2, 4, 0, 0, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
+                                  kf, kend);
+            // Stage s+1 has landed (all waves) and every wave's reads of
+            // stage s are complete, so the next iteration may refill it.
+            __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+            barrier_no_fence();
+            mfma_rows<3, 4, 0, 0, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
+                                  kf, kend);
+            cur = nxt;
+        }
+    }
+}
+
+// Fast path: one BM x BN output tile per workgroup, operands streamed through
+// LDS by DMA (k_pipeline), epilogue staged through LDS.
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS>
 __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -780,7 +864,6 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     using OpB = DmaOperand<B_K, BN, NT, SN, BK>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
     constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
-    constexpr int kSteps = BK / 16;
     __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
     const uint32_t tid = threadIdx.x;
@@ -818,70 +901,15 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
         for (int j = 0; j < SN; ++j) acc[i][j] = f32x16_t{};
 
     if (nst > 0) {
-        bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
         const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-        if constexpr (BK == 32) {
-            // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
-#pragma unroll
-            for (int s = 0; s < NS - 1; ++s) {
-                la.issue(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * BK, kend);
-                lb.issue(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * BK, kend);
-            }
-            T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
-            barrier_no_fence();
-            la.template read<0>(lds0, fa0);
-            lb.template read<0>(lds0 + A_BYTES, fb0);
-
-            constexpr int kHalf = (kVmemPerStage + 1) / 2;
-            uint32_t cur = 0;                 // byte offset of stage s's buffer
-            uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
-            for (int s = 0; s < nst; ++s) {
-                const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
-                const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * BK;
-                const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
-                const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-                // K step 0 of stage s (reads: step 1 of stage s), then K step 1
-                // (reads: step 0 of stage s+1, landed before the last barrier).
-                mfma_rows<0, 2, 0, kHalf>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill,
-                                          ra, rb, kf, kend);
-                mfma_rows<1, 2, kHalf, kVmemPerStage - kHalf>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                               lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
-                T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
-                barrier_no_fence();
-                fill = cur;
-                cur = nxt;
-            }
-        } else {
-            static_assert(kSteps == 4, "BK 64 has four K steps");
-            la.issue(lds0, p.a, a_bytes, p.lda, kbeg, kend);
-            lb.issue(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
-            T0G_WAIT_VMCNT(0);
-            barrier_no_fence();
-            la.template read<0>(lds0, fa0);
-            lb.template read<0>(lds0 + A_BYTES, fb0);
-
-            constexpr int kHalf = (kVmemPerStage + 1) / 2;
-            uint32_t cur = 0;
-            for (int s = 0; s < nst; ++s) {
-                const uint32_t nxt = cur ^ STAGE;   // the other buffer, freed by the previous barrier
-                const uint32_t kf = kbeg + (uint32_t)(s + 1) * BK;
-                const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
-                const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-                mfma_rows<0, 4, 0, kHalf>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
-                                          ra, rb, kf, kend);
-                mfma_rows<1, 4, kHalf, kVmemPerStage - kHalf>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                               lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
-                mfma_rows<2, 4, 0, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                      kf, kend);
-                // Stage s+1 has landed (all waves) and every wave's reads of
-                // stage s are complete, so the next iteration may refill it.
-                __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
-                barrier_no_fence();
-                mfma_rows<3, 4, 0, 0>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                      kf, kend);
-                cur = nxt;
-            }
-        }
+        // Stages past a K tail need masked DMA; whole stages (the usual case)
+        // skip the per-lane bound test.
+        if ((kend - kbeg) % BK == 0)
+            k_pipeline<false, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
+                                                                      nst, lds0);
+        else
+            k_pipeline<true, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
+                                                                     nst, lds0);
     }
 
     // Epilogue through LDS: 16-byte row stores for tiles wholly inside an

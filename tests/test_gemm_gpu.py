@@ -167,6 +167,28 @@ def test_no_writes_outside_the_output(rt, bufs, preset, m):
     assert np.all(got[:m, n:] == -9999.0), "columns >= N were written"
 
 
+@pytest.mark.parametrize("preset", PRESETS)
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 200), (512, 256, 72), (300, 264, 128), (264, 520, 8)])
+def test_k_tails_and_edge_tiles(rt, bufs, preset, layout, m, n, k):
+    """K not a multiple of the stage depth (masked DMA of the K tail) on whole
+    tiles, and whole stages on ragged M/N tiles (element-wise epilogue), with
+    the bias+ReLU epilogue; fp32 and bf16 output."""
+    _log(f"[case] k-tail {preset} {layout} {m}x{n}x{k}")
+    a_mk = o.rand_bf16_xorshift(m * k, 7 * m + k).reshape(m, k)
+    b_nk = o.rand_bf16_xorshift(n * k, 11 * n + k).reshape(n, k)
+    bias = np.linspace(-2.0, 2.0, n).astype(np.float32)
+    ref = np.maximum(o.gemm_nt_naive(a_mk, b_nk, m, k, n) + bias[None, :], 0.0).astype(np.float32)
+    a_st, b_st = stored_operands(layout, a_mk, b_nk)
+    bp = bufs.up(bias)
+    cfg = t0g.GemmConfig.preset(preset)
+    c32 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, config=cfg, epilogue=t0g.EPI_BIAS_ADD_RELU, bias=bp)
+    check_parity(c32, ref, k, f"k-tail {preset} {layout} {m}x{n}x{k}")
+    c16 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, out=t0g.BF16, config=cfg,
+                   epilogue=t0g.EPI_BIAS_ADD_RELU, bias=bp)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c32)), "bf16 output != RNE(fp32 output)"
+
+
 def test_all_ones_known_answer(rt, bufs):
     """examples/hello_gemm_gen.rs:72-133: bf16(1.0) inputs give C = K exactly."""
     for (m, k, n) in [(256, 4096, 256), (128, 1024, 4096), (512, 512, 512)]:
