@@ -739,6 +739,16 @@ __device__ __forceinline__ void barrier_no_fence() {
 // and with DMA instructions [DFIRST, DFIRST + DCOUNT) of the stage being
 // filled.  sched_barrier pins the row order, so MFMAs stay queued while a DMA
 // instruction issues.
+// Per row of MFMAs, the DMA instructions and fragment reads are placed one at
+// a time behind individual MFMAs (DMA, read, DMA, read, ...), so no two long
+// issues sit between consecutive MFMAs.  Item t of a row with nd DMAs and nr
+// reads: kind 0 = DMA, 1 = read; returns kind * 256 + index.
+__host__ __device__ constexpr int row_item(int t, int nd, int nr) {
+    const int both = nd < nr ? nd : nr;
+    if (t < 2 * both) return (t & 1) * 256 + (t >> 1);
+    return nd > nr ? (t - both) : 256 + (t - both);
+}
+
 template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, bool CHECK, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
                                           bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
@@ -751,29 +761,37 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
     // needs all of B but only A[0]), spread evenly over the rows.
     constexpr int kReads = SM + SN;
     constexpr int kReadsPerRow = (kReads + SM - 1) / SM;
+    constexpr int kItems = kPerRow + kReadsPerRow;
+    constexpr int kPerSlot = (kItems + SN - 1) / SN;
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
 #pragma unroll
-        for (int d = 0; d < kReadsPerRow; ++d) {
-            const int q = i * kReadsPerRow + d;
-            if (q < SN)
-                nb[q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, q);
-            else if (q < kReads)
-                na[q - SN] = la.template read_one<NEXT_KK>(rd, q - SN);
-        }
+        for (int j = 0; j < SN; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < SN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int d = 0; d < kPerRow; ++d) {
-            const int q = DFIRST + i * kPerRow + d;
-            if (q < DFIRST + DCOUNT) {
-                if (q < OpA::kInstr)
-                    la.template issue_one<CHECK>(q, ra, fill, kf, kend);
-                else
-                    lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+            for (int u = 0; u < kPerSlot; ++u) {
+                const int t = j * kPerSlot + u;
+                if (t < kItems) {
+                    const int it = row_item(t, kPerRow, kReadsPerRow);
+                    if (it >= 256) {
+                        const int q = i * kReadsPerRow + (it - 256);
+                        if (q < SN)
+                            nb[q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, q);
+                        else if (q < kReads)
+                            na[q - SN] = la.template read_one<NEXT_KK>(rd, q - SN);
+                    } else {
+                        const int q = DFIRST + i * kPerRow + it;
+                        if (q < DFIRST + DCOUNT) {
+                            if (q < OpA::kInstr)
+                                la.template issue_one<CHECK>(q, ra, fill, kf, kend);
+                            else
+                                lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+                        }
+                    }
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

@@ -31,13 +31,16 @@ int ok() {
 }
 
 // MI355X tile set.  Every entry has a precompiled kernel family in
-// t0g_gemm_gfx950.hsaco (gemm_gfx950.hip).  `eff` is the sustained fraction of
-// the per-CU MFMA rate the tile reaches when the CU is full, `wg_per_cu` how
-// many of its workgroups fit one CU (LDS 2*(BM+BN)*128 B, registers).
+// t0g_gemm_gfx950.hsaco (gemm_gfx950.hip).  The timing fields were fitted to
+// kernel times measured on one MI355X (bf16 in, bf16 out, random data, so at
+// the power-limited shader clock that data draws): time per wave of
+// workgroups = t0_us + (per-CU FLOP) / rate, linear in K to within a few
+// percent over K = 256 .. 8192.  64x64 gains throughput from co-resident
+// workgroups, 128x128 does not (one already saturates the CU's LDS traffic).
 const TileDef kTiles[kNumTiles] = {
-    {256, 256, 256, 0.80, 1, "t0g_gemm_256x256_k64"},
-    {128, 128, 256, 0.60, 2, "t0g_gemm_128x128_k64"},
-    {64, 64, 256, 0.30, 2, "t0g_gemm_64x64_k64"},
+    {256, 256, 256, 1, 13.9, 5243.0, 5243.0, "t0g_gemm_256x256_k64"},
+    {128, 128, 256, 2, 6.7, 3034.0, 3034.0, "t0g_gemm_128x128_k64"},
+    {64, 64, 256, 4, 2.6, 931.0, 1606.0, "t0g_gemm_64x64_k64"},
 };
 
 const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size) {
@@ -85,23 +88,28 @@ int validate(const t0g_gemm_config *cfg) {
 }
 
 // ---- selection model ---------------------------------------------------------
-// Modelled time of one (tile, split) choice on MI355X: 256 CUs, 2.5 PF dense
-// bf16, 8 TB/s HBM.  Each CU holds up to wg_per_cu workgroups that share its
-// MFMA rate; the busiest CU's share of the work sets the compute time.  Memory
-// time counts compulsory operand and output bytes plus split-K workspace
-// traffic; a split-K reduce costs an extra launch.
+// Modelled time (us) of one (tile, split) choice on MI355X's 256 CUs.  The
+// busiest CU runs ceil(WGs / 256) workgroups, up to wg_per_cu at once; each
+// wave of them costs t0_us, and their FLOPs go at the tile's per-CU rate for
+// that occupancy.  Compulsory HBM bytes at 8 TB/s bound it from below.  A
+// split-K adds the fp32 plane traffic and the reduce launch (fitted: 2.5 us +
+// planes read at 4.5 TB/s + 0.25 us per plane of latency).
 double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk) {
     const double tiles = (double)((m + t.bm - 1) / t.bm) * (double)((n + t.bn - 1) / t.bn);
-    const uint32_t kc = ((k + sk - 1) / sk + kTileK - 1) / kTileK * kTileK;
+    const double kc = (double)(((k + sk - 1) / sk + kTileK - 1) / kTileK * kTileK);
     const double wgs = tiles * sk;
-    const double per_cu = ceil(wgs / kNumCUs);   // workgroups on the busiest CU
-    const double cu_rate = kPeakFlops / kNumCUs * t.eff;
-    const double t_comp = per_cu * (2.0 * t.bm * t.bn * (double)(kc > 0 ? kc : kTileK)) / cu_rate;
-    double bytes = 2.0 * ((double)m * k + (double)k * n) + 4.0 * (double)m * n;
-    if (sk > 1) bytes += 8.0 * (double)m * n * sk;
-    const double t_mem = bytes / kPeakBytes;
-    double t_us = (t_comp > t_mem ? t_comp : t_mem) * 1e6;
-    if (sk > 1) t_us += 2.0;   // second launch
+    const double per_cu = ceil(wgs / kNumCUs);
+    const double resident = per_cu < t.wg_per_cu ? per_cu : (double)t.wg_per_cu;
+    const double waves = ceil(per_cu / t.wg_per_cu);
+    const double rate = t.wg_per_cu > 1
+                            ? t.rate1 + (t.rate_full - t.rate1) * (resident - 1.0) / (double)(t.wg_per_cu - 1)
+                            : t.rate1;
+    const double flops_cu = per_cu * 2.0 * t.bm * t.bn * (kc > 0 ? kc : (double)kTileK);
+    double t_us = waves * t.t0_us + flops_cu / rate * 1e-3;
+    const double bytes = 2.0 * ((double)m * k + (double)k * n) + 2.0 * (double)m * n;
+    const double t_mem = bytes / kPeakBytes * 1e6;
+    if (t_mem > t_us) t_us = t_mem;
+    if (sk > 1) t_us += 2.5 + (double)sk * m * n * 4.0 / 4.5e6 + 0.25 * sk;
     return t_us;
 }
 

@@ -17,10 +17,14 @@ constexpr uint32_t kMaxSplitK = 64;
 constexpr double kPeakFlops = 2.5e15;   // dense bf16 MFMA, MI355X
 constexpr double kPeakBytes = 8.0e12;   // HBM3E, MI355X
 
+// One entry of the MI355X tile table (see kTiles for the meaning of the
+// timing fields).
 struct TileDef {
     uint32_t bm, bn, wg;
-    double eff;
-    uint32_t wg_per_cu;
+    uint32_t wg_per_cu;     // workgroups one CU holds at once (LDS, registers)
+    double t0_us;           // per-wave fixed cost: prologue, epilogue, launch share
+    double rate1;           // per-CU bf16 FLOP/ns with one resident workgroup
+    double rate_full;       // per-CU bf16 FLOP/ns with wg_per_cu resident workgroups
     const char *symbol_prefix;
 };
 constexpr int kNumTiles = 3;
