@@ -136,8 +136,9 @@ def cpu_baseline(torch, tensors, m, n, k, min_seconds):
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed launches first; the shader clock needs ~20 ms of load to settle")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
@@ -229,7 +230,7 @@ def main():
         extra = {}
         steps8 = max(5, args.steps // 2)
         log(f"[bench] 8192^3 NN bf16: steps {steps8}")
-        r8 = time_gemm(t0g, torch, rt, stream, 8192, 8192, 8192, "NN", steps8, 3, seed=4)
+        r8 = time_gemm(t0g, torch, rt, stream, 8192, 8192, 8192, "NN", steps8, max(3, args.warmup // 8), seed=4)
         t8 = r8["flop"] / (r8["event_ms_per_launch"] * 1e-3) / 1e12
         extra["gemm_nn_8192^3"] = {"tflops": round(t8, 2), "frac_of_peak": round(t8 / PEAK_TFLOPS, 4),
                                    "ms_per_launch": round(r8["event_ms_per_launch"], 4), "kernel": r8["kernel"]}
@@ -248,7 +249,8 @@ def main():
                            "frac_of_hbm": round(r["bytes_min"] / sec / 1e9 / PEAK_GBS, 4),
                            "us_per_gemm": round(sec * 1e6, 2), "kernel": r["kernel"]}
         log("[bench] MLP step")
-        extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5), 2)
+        extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
+                                                     max(2, args.warmup // 10))
         line["extra"] = extra
 
     if args.cpu_seconds > 0:

@@ -749,38 +749,51 @@ __host__ __device__ constexpr int row_item(int t, int nd, int nr) {
     return nd > nr ? (t - both) : 256 + (t - both);
 }
 
-template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, bool CHECK, int SM, int SN, class OpA, class OpB>
+template <int STEP, int NSTEPS, int DFIRST, int DCOUNT, bool CHECK, int RB = 0, int RE = -1, int RR = 0, int SM,
+          int SN, class OpA, class OpB>
 __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
                                           bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
                                           uint32_t cur, uint32_t nxt, uint32_t fill, u32x4_t ra, u32x4_t rb,
                                           uint32_t kf, uint32_t kend) {
+    // Rows [RB, RE) of the step; the next step's fragment reads go to rows
+    // [RR, RE) (all of them: a step split in two calls gives the reads to the
+    // second), the DMA instructions are spread over all rows of this call.
+    constexpr int kRE = RE < 0 ? SM : RE;
     constexpr int NEXT_KK = (STEP + 1) % NSTEPS;
     const uint32_t rd = STEP + 1 < NSTEPS ? cur : nxt;
-    constexpr int kPerRow = (DCOUNT + SM - 1) / SM;
-    // Fragment reads of the next step, B first (the next step's first row
-    // needs all of B but only A[0]), spread evenly over the rows.
-    constexpr int kReads = SM + SN;
-    constexpr int kReadsPerRow = (kReads + SM - 1) / SM;
-    constexpr int kItems = kPerRow + kReadsPerRow;
-    constexpr int kPerSlot = (kItems + SN - 1) / SN;
+    constexpr int kRows = kRE - RB;
+    constexpr int kPerRow = (DCOUNT + kRows - 1) / kRows;
+    // Read placement: the next step's row r needs A[r] and all of B, so A[r]
+    // is read in row r and B two fragments per row from the first read row
+    // on: every fragment then has at least three rows of MFMAs to land.
+    constexpr int kReadRows = kRE - RR;
 #pragma unroll
-    for (int i = 0; i < SM; ++i) {
+    for (int i = RB; i < kRE; ++i) {
+        const int bfirst = kReadRows > 0 ? 2 * (i - RR) : SN;
+        const int blast = i == kRE - 1 ? SN : 2 * (i - RR) + 2;   // the last read row takes any B left
+        const int nbr = i < RR ? 0 : (blast < SN ? blast : SN) - (bfirst < SN ? bfirst : SN);
+        const int nar = i < RR ? 0 : (kReadRows == SM ? 1 : (i == RR ? SM : 0));
+        const int nr = nbr + nar;
+        const int nitems = kPerRow + nr;
+        const int per_slot = (nitems + SN - 1) / SN;
 #pragma unroll
         for (int j = 0; j < SN; ++j) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < kPerSlot; ++u) {
-                const int t = j * kPerSlot + u;
-                if (t < kItems) {
-                    const int it = row_item(t, kPerRow, kReadsPerRow);
+            for (int u = 0; u < per_slot; ++u) {
+                const int t = j * per_slot + u;
+                if (t < nitems) {
+                    const int it = row_item(t, kPerRow, nr);
                     if (it >= 256) {
-                        const int q = i * kReadsPerRow + (it - 256);
-                        if (q < SN)
-                            nb[q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, q);
-                        else if (q < kReads)
-                            na[q - SN] = la.template read_one<NEXT_KK>(rd, q - SN);
+                        const int q = it - 256;   // B reads of this row first, then its A reads
+                        if (q < nbr)
+                            nb[bfirst + q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, bfirst + q);
+                        else if (kReadRows == SM)
+                            na[i] = la.template read_one<NEXT_KK>(rd, i);
+                        else
+                            na[q - nbr] = la.template read_one<NEXT_KK>(rd, q - nbr);
                     } else {
-                        const int q = DFIRST + i * kPerRow + it;
+                        const int q = DFIRST + (i - RB) * kPerRow + it;
                         if (q < DFIRST + DCOUNT) {
                             if (q < OpA::kInstr)
                                 la.template issue_one<CHECK>(q, ra, fill, kf, kend);
@@ -853,17 +866,17 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
             const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
             const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
             mfma_rows<0, 4, 0, kHalf, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
-                                      ra, rb, kf, kend);
+                                             ra, rb, kf, kend);
             mfma_rows<1, 4, kHalf, kVmemPerStage - kHalf, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                           lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
+                                                                 lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
             mfma_rows<2, 4, 0, 0, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                  kf, kend);
+                                         kf, kend);
             // Stage s+1 has landed (all waves) and every wave's reads of
             // stage s are complete, so the next iteration may refill it.
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
             barrier_no_fence();
             mfma_rows<3, 4, 0, 0, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                  kf, kend);
+                                         kf, kend);
             cur = nxt;
         }
     }
