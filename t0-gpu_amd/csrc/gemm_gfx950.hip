@@ -811,7 +811,8 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
 // The K loop of the fast path.  BK 32: ring of NS >= 4 stages, DMA NS-1
 // stages ahead, one barrier per stage.  BK 64: NS = 2 (double buffer): the DMA
 // of stage s+1 is issued during the first half of stage s and retired, with one
-// barrier, before the stage's last K step reads stage s+1's first fragments.
+// barrier, halfway through the stage's last K step, before its second half reads
+// stage s+1's first fragments.
 template <bool CHECK, uint32_t BK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN,
           class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& la, const OpB& lb, const T0gGemmArgs& p,
@@ -871,12 +872,16 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
                                                                  lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
             mfma_rows<2, 4, 0, 0, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
                                          kf, kend);
-            // Stage s+1 has landed (all waves) and every wave's reads of
-            // stage s are complete, so the next iteration may refill it.
+            // Rows 0-1 of the last step need no new data, which gives the DMA
+            // half a step more.  Then stage s+1 must have landed (all waves)
+            // before rows 2-3 read its first fragments, and every wave's reads
+            // of stage s are complete, so the next iteration may refill it.
+            mfma_rows<3, 4, 0, 0, CHECK, 0, 2, 2>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
+                                                  ra, rb, kf, kend);
             __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
             barrier_no_fence();
-            mfma_rows<3, 4, 0, 0, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                         kf, kend);
+            mfma_rows<3, 4, 0, 0, CHECK, 2, 4, 2>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
+                                                  ra, rb, kf, kend);
             cur = nxt;
         }
     }
