@@ -950,7 +950,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
 
     // Epilogue through LDS: 16-byte row stores for tiles wholly inside an
     // aligned C, per-element masked stores otherwise.
-    static_assert(4 * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
+    static_assert((NT / 64) * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
     T0G_WAIT_VMCNT(0);    // LDS DMA still in flight (stages past K) has landed
     barrier_no_fence();   // and every wave is done with the ring
     const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
