@@ -960,24 +960,64 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the
 // order the reference's host loop uses (examples/test_gemm_correctness.rs:190-207),
-// then the epilogue and the output conversion.
+// then the epilogue and the output conversion.  Vector form (T0G_REDUCE_VEC):
+// each thread owns 4 consecutive columns, loads up to 8 planes' float4 at once
+// (all in flight together) and adds them in plane order.
 template <bool OUT_BF16>
 __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
-    const float* __restrict__ ws = reinterpret_cast<const float*>(p.ws);
-    const float* __restrict__ bias = reinterpret_cast<const float*>(p.bias);
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    const __attribute__((address_space(1))) float* ws = reinterpret_cast<const __attribute__((address_space(1))) float*>(p.ws);
+    const __attribute__((address_space(1))) float* bias =
+        reinterpret_cast<const __attribute__((address_space(1))) float*>(p.bias);
+    if (p.flags & T0G_REDUCE_VEC) {
+        const uint32_t nq = p.n >> 2;
+        const uint32_t total = p.m * nq;
+        for (uint32_t q = blockIdx.x * 256 + threadIdx.x; q < total; q += p.grid_blocks * 256) {
+            const uint32_t row = q / nq, col = (q - row * nq) * 4;
+            const uint64_t w = (uint64_t)row * p.ldw + col;
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
+                f32x4_t v[8];
+#pragma unroll
+                for (uint32_t u = 0; u < 8; ++u)
+                    if (s0 + u < p.splits)
+                        v[u] = *reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>(
+                            ws + (s0 + u) * p.plane_elems + w);
+#pragma unroll
+                for (uint32_t u = 0; u < 8; ++u)
+                    if (s0 + u < p.splits) acc = acc + v[u];
+            }
+            float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = apply_epilogue(x[c], p.epilogue != 0 ? bias[col + c] : 0.0f, p.epilogue);
+            const uint64_t o = (uint64_t)row * p.ldc + col;
+            if constexpr (OUT_BF16) {
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                u32x2_t w2;
+                w2[0] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[0]) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[1]) << 16);
+                w2[1] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2]) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[3]) << 16);
+                *reinterpret_cast<__attribute__((address_space(1))) u32x2_t*>((uintptr_t)(p.c + o * 2)) = w2;
+            } else {
+                const f32x4_t y = {x[0], x[1], x[2], x[3]};
+                *reinterpret_cast<__attribute__((address_space(1))) f32x4_t*>((uintptr_t)(p.c + o * 4)) = y;
+            }
+        }
+        return;
+    }
     const size_t total = (size_t)p.m * p.n;
     for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)p.grid_blocks * 256) {
         const uint32_t row = (uint32_t)(idx / p.n), col = (uint32_t)(idx % p.n);
         const size_t w = (size_t)row * p.ldw + col;
         float acc = 0.0f;
         for (uint32_t s = 0; s < p.splits; ++s) acc = acc + ws[s * p.plane_elems + w];
-        if (p.epilogue != 0) acc = acc + bias[col];
-        if (p.epilogue == 2) acc = acc > 0.0f ? acc : 0.0f;
+        acc = apply_epilogue(acc, p.epilogue != 0 ? bias[col] : 0.0f, p.epilogue);
         const size_t o = (size_t)row * p.ldc + col;
         if constexpr (OUT_BF16)
-            reinterpret_cast<__bf16*>(p.c)[o] = (__bf16)acc;
+            reinterpret_cast<gbf16_t*>((uintptr_t)p.c)[o] = (__bf16)acc;
         else
-            reinterpret_cast<float*>(p.c)[o] = acc;
+            reinterpret_cast<gf32_t*>((uintptr_t)p.c)[o] = acc;
     }
 }
 

@@ -32,10 +32,11 @@ typedef struct T0gReduceArgs {
     uint32_t splits;
     uint32_t epilogue;
     uint32_t grid_blocks;    /* launched workgroups (256 threads each)           */
-    uint32_t pad_;
+    uint32_t flags;          /* T0G_REDUCE_VEC                                    */
 } T0gReduceArgs;
 
 #define T0G_FLAG_XCD_REMAP 1u   /* remap block ids so each XCD owns a contiguous tile range */
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
+#define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
 
 #endif

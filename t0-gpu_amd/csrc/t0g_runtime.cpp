@@ -303,7 +303,11 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     r.ldc = o.ldc;
     r.splits = p.splits;
     r.epilogue = o.epilogue;
-    const uint64_t total = (uint64_t)o.m * o.n;
+    const uint64_t out_esize = p.out_bf16 ? 2 : 4;
+    const bool vec = (ws & 15) == 0 && (o.n & 3) == 0 && (o.c & (4 * out_esize - 1)) == 0 &&
+                     ((uint64_t)o.ldc * out_esize) % (4 * out_esize) == 0 && (uint64_t)o.m * (o.n / 4) < (1ull << 31);
+    if (vec) r.flags |= T0G_REDUCE_VEC;
+    const uint64_t total = vec ? (uint64_t)o.m * (o.n / 4) : (uint64_t)o.m * o.n;
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     r.grid_blocks = (uint32_t)blocks;

@@ -241,6 +241,38 @@ def test_c4b_split_k(rt, bufs, split_k):
     assert np.array_equal(c16, o.f32_to_bf16_rne(c1))
 
 
+@pytest.mark.parametrize("m,n,k,sk,out", [(256, 256, 32768, 16, t0g.F32), (256, 256, 32768, 16, t0g.BF16),
+                                           (100, 66, 2048, 8, t0g.F32), (100, 66, 2048, 8, t0g.BF16),
+                                           (128, 4096, 4096, 8, t0g.BF16)])
+def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
+    """The on-device reduce equals the reference's host loop (plane order, from
+    0.0, fp32) applied to the same partial planes, bit for bit; N % 4 != 0
+    takes the element-wise reduce, the others the 4-wide one."""
+    _log(f"[case] reduce order {m}x{n}x{k} sk={sk} out={out}")
+    a_mk = o.rand_bf16_lcg(m * k, 5 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 9 + n).reshape(n, k)
+    a = bufs.up(a_mk)
+    b = bufs.up(b_nk)
+    esz = 4 if out == t0g.F32 else 2
+    c = bufs.alloc(m * n * esz, fill=0)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk)
+    need = t0g.gemm_workspace_size(d)
+    assert need >= sk * m * n * 4
+    ws = bufs.alloc(need, fill=0)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk, workspace=ws,
+                      workspace_bytes=need)
+    rt.gemm_desc(d)
+    rt.wait_idle()
+    planes = rt.read(ws, (sk, m, n), np.float32)
+    host = o.splitk_reduce(planes)
+    got = rt.read(c, (m, n), np.float32 if out == t0g.F32 else np.uint16)
+    if out == t0g.F32:
+        assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
+    else:
+        assert np.array_equal(got, o.f32_to_bf16_rne(host))
+    check_parity(host, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"reduce order {m}x{n}x{k}")
+
+
 def _randn_pair(m, n, k, seed_a=2, seed_b=3):
     a = o.randn_bf16(m * k, seed_a, 0.02)
     b = o.randn_bf16(k * n, seed_b, 0.02)
