@@ -1063,11 +1063,31 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
     T0G_GEMM_LAYOUTS(PFX, BM, BN, WM, WN, f32, false, _u, false) \
     T0G_GEMM_LAYOUTS(PFX, BM, BN, WM, WN, bf16, true, _u, false)
 
+// Deep-ring variant (suffix _d) of the 64x64 tile for grids of at most one
+// workgroup per CU (split-K shapes): 128 KB of LDS per workgroup keeps 15
+// stages of DMA in flight instead of 3, covering HBM latency with a single
+// workgroup on the CU.
+#define T0G_PIPE_D_64x64 32, 16
+#define T0G_GEMM_D(NAME, BM, BN, WM, WN, AK, BKM, OBF)                                                           \
+    extern "C" __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))       \
+        NAME(T0gGemmArgs p) {                                                                                  \
+        t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_D_##BM##x##BN>(p);                           \
+    }
+#define T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, OUTN, OBF)                  \
+    T0G_GEMM_D(PFX##_nt_##OUTN##_d, BM, BN, WM, WN, true, true, OBF)        \
+    T0G_GEMM_D(PFX##_nn_##OUTN##_d, BM, BN, WM, WN, true, false, OBF)       \
+    T0G_GEMM_D(PFX##_tn_##OUTN##_d, BM, BN, WM, WN, false, false, OBF)      \
+    T0G_GEMM_D(PFX##_tt_##OUTN##_d, BM, BN, WM, WN, false, true, OBF)
+#define T0G_GEMM_TILE_D(PFX, BM, BN, WM, WN)                \
+    T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, f32, false)     \
+    T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, bf16, true)
+
 T0G_GEMM_TILE(t0g_gemm_256x256_k64, 256, 256, 2, 2)
 T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_64x64_k64, 64, 64, 2, 2)
+T0G_GEMM_TILE_D(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 
 extern "C" __global__ void __launch_bounds__(256) t0g_splitk_reduce_f32(T0gReduceArgs p) {
     t0g::splitk_reduce<false>(p);

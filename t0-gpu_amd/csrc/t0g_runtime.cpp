@@ -211,8 +211,13 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, boo
     p->splits = sk;
     p->k_per_split = kps;
     const bool partial = sk > 1;
+    // At most one workgroup per CU: the 64x64 tile switches to its deep-ring
+    // variant (the CU's LDS then holds one workgroup with 128 KB of stages;
+    // measured 10 % faster on 256x256x32768 split 16, while 128x128 gained
+    // nothing on 128x4096x4096 split 8 and keeps its 4-stage ring).
+    const bool deep = aligned && tile->bm == 64 && (uint64_t)p->tiles_m * p->tiles_n * sk <= kNumCUs;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
-                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? "" : "_u");
+                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (deep ? "_d" : "") : "_u");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
     return T0G_OK;

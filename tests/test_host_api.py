@@ -142,7 +142,7 @@ def test_gemm_plan_selection_host_only():
     d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 33, 50, 100)          # K % 8 != 0: element-wise loads
     assert t0g.gemm_kernel_name(d).endswith("_u")
     d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 256, 256, 32768)
-    assert t0g.gemm_kernel_name(d).endswith("_nt_f32")
+    assert "_nt_f32" in t0g.gemm_kernel_name(d)            # split-K: f32 partial planes
     ws = t0g.gemm_workspace_size(d)
     cfg = t0g.auto_select(256, 32768, 256)
     assert ws == cfg.split_k * 256 * 256 * 4
