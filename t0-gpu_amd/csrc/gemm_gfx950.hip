@@ -346,7 +346,9 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
 #pragma unroll
                     for (int c = 0; c < 4; ++c) w[c] = __builtin_bit_cast(uint32_t, v[c]);
                 }
-                *reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr) = w;
+                // Non-temporal: C is not read again here, so keep it from
+                // evicting A/B panels that later tiles on this XCD still need.
+                __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
             } else if (grow < p.m) {
 #pragma unroll
                 for (int c = 0; c < kCols; ++c) {
