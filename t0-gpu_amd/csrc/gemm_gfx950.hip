@@ -27,6 +27,10 @@
 
 #include "t0g_kernel_args.h"
 
+#ifndef T0G_MFMA16
+#define T0G_MFMA16 1
+#endif
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // Global-memory pointer types: with an explicit address space the compiler
 // emits global_* instead of flat_* instructions (flat loads also count on
@@ -889,6 +893,12 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
     }
 }
 
+}  // namespace t0g
+
+#include "gemm_mfma16.h"
+
+namespace t0g {
+
 // Fast path: one BM x BN output tile per workgroup, operands streamed through
 // LDS by DMA (k_pipeline), epilogue staged through LDS.
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS>
@@ -1045,7 +1055,9 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 #define T0G_GEMM(NAME, BM, BN, WM, WN, AK, BKM, OBF, AL)                                       \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                   \
         __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmArgs p) {          \
-        if constexpr (AL)                                                                        \
+        if constexpr (AL && BM == 256 && T0G_MFMA16)                                             \
+            t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                              \
+        else if constexpr (AL)                                                                   \
             t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_##BM##x##BN>(p);            \
         else                                                                                     \
             t0g::gemm_tile<BM, BN, WM, WN, AK, BKM, OBF, AL>(p);                                 \

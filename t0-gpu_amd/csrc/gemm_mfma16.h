@@ -1,0 +1,459 @@
+// 16x16x32 MFMA variant of the fast path, used for the 256x256 tile.
+//
+// Included by gemm_gfx950.hip after its DMA, swizzle and epilogue helpers.
+// Same tiling as the 32x32x16 path (4 waves of 128x128, two 64 KB stages of
+// 64 K values streamed into LDS by DMA), but each wave issues 64
+// v_mfma_f32_16x16x32_bf16 per 32-wide K step on 8 x 8 sub-tiles of 16x16.
+// At MI355X's board power limit the 16x16x32 form sustains a higher shader
+// clock for the same FLOP rate per clock (it moves a quarter of the
+// accumulator registers per instruction), so the GEMM gets more FLOP/s.
+//
+// MFMA operand layout (16x16x32 bf16): lane l holds A[l % 16][8*(l/16) .. +7]
+// and B[8*(l/16) .. +7][l % 16]; the result lane l holds D[4*(l/16) + r][l % 16],
+// r = 0..3.
+#ifndef T0G_GEMM_MFMA16_H
+#define T0G_GEMM_MFMA16_H
+
+namespace t0g {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// M/N-contiguous granule swizzle for the 16-wide fragments: {0,2,5,7}[k % 4]
+// flipped by bit 3 of k, so the two 16-lane groups of a ds_read_b64_tr_b16
+// half-wave (k rows 8 apart, same 16 columns) use the other 4 granules of the
+// 256-byte bank window.
+__device__ __forceinline__ uint32_t fm16(uint32_t k, uint32_t granules) {
+    return (((0x7520u >> ((k & 3u) * 4)) & 0xFu) ^ ((k >> 3) & 1u)) & (granules - 1);
+}
+
+// DMA of one 16-byte piece per lane at voff + add: the add is done inside
+// the asm block so the per-instruction offsets are not kept in registers.
+__device__ __forceinline__ void dma16_add(u32x4_t rsrc, uint32_t voff, uint32_t add, uint32_t lds_m0) {
+    uint32_t tmp;
+    asm volatile(
+        "v_add_u32 %0, %1, %2\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %3, 0 offen lds"
+        : "=&v"(tmp)
+        : "s"(add), "v"(voff), "s"(rsrc), "s"(lds_m0)
+        : "memory", "m0");
+}
+
+template <bool K_MAJOR, int ROWS, int NT, int SUBS>
+struct Op16;
+
+// K-contiguous operand of a 256-row tile, 64 K values per stage: 128-byte LDS
+// rows, chunk swizzle fk<64>.  DMA instruction i of a wave covers rows
+// 32 i + 8 wave + lane / 8; fk<64> of those rows does not depend on i, so one
+// offset register and one K column serve all of a wave's instructions.
+template <int ROWS, int NT, int SUBS>
+struct Op16<true, ROWS, NT, SUBS> {
+    static constexpr int kWaves = NT / 64;
+    static constexpr uint32_t kKRow = 128;
+    static constexpr int kInstr = ROWS * kKRow / 1024 / kWaves;
+    static_assert(ROWS == 256 && kWaves == 4, "offset sharing assumes a 256-row tile and 4 waves");
+    static constexpr uint32_t kStageBytes = ROWS * kKRow;
+    uint32_t off0;    // byte offset of instruction 0's piece at k = 0
+    uint32_t kcol;    // first K column of the lane's piece
+    uint32_t step;    // bytes between instructions (32 rows)
+    uint32_t wave;
+    uint32_t frag[2];   // per 32-wide K step: LDS offset of the lane's chunk in sub-tile 0
+
+    __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t lane = tid & 63u;
+        const uint32_t r = 8 * wave + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ fk<64>(r);
+        kcol = c * 8;
+        off0 = ((row0 + r) * ld + c * 8) * 2;
+        step = 64 * ld;
+        const uint32_t row = wrow + (lane & 15u), qk = lane >> 4;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) frag[kk] = row * kKRow + (((4u * kk + qk) ^ fk<64>(row)) << 4);
+    }
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t, uint32_t k0) const {
+        return rsrc_words(base, bytes, (uint64_t)k0 * 2);
+    }
+    template <bool CHECK>
+    __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
+        const uint32_t m0 = lds + (i * kWaves + wave) * 1024;
+        if (CHECK)
+            dma16(r, k0 + kcol < kend ? off0 + i * step : kOob, m0);
+        else
+            dma16_add(r, off0, i * step, m0);
+    }
+    template <bool CHECK>
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
+                                          uint32_t kend) const {
+        const u32x4_t r = rsrc(base, bytes, ld, k0);
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
+    }
+    // Fragment of 16-row sub-tile `sub` for 32-wide K step KK.
+    template <int KK>
+    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
+        return lds_load_b128(stage + frag[KK] + sub * 16 * kKRow);
+    }
+};
+
+// M/N-contiguous operand of a 256-column tile: LDS rows are k rows of 512
+// bytes, granule swizzle fm16.  DMA instruction i of a wave covers k rows
+// 8 i + 2 wave + lane / 32; their swizzle differs only by bit 0 of i, so two
+// offset registers serve all of a wave's instructions.
+template <int ROWS, int NT, int SUBS>
+struct Op16<false, ROWS, NT, SUBS> {
+    static constexpr int kWaves = NT / 64;
+    static constexpr uint32_t kRowB = ROWS * 2;
+    static constexpr uint32_t kGranules = ROWS / 16;
+    static constexpr uint32_t kStageBytes = 64 * kRowB;
+    static constexpr int kInstr = kStageBytes / 1024 / kWaves;
+    static_assert(ROWS == 256 && kWaves == 4, "offset sharing assumes a 256-column tile and 4 waves");
+    uint32_t off[2];   // byte offsets of instructions 0 and 1 (less one instruction step) at k = 0
+    uint32_t krow;     // k row of instruction 0's piece
+    uint32_t step;     // bytes between instructions (8 k rows)
+    uint32_t wave;
+    uint32_t frag0;    // K step 0, half 0, sub-tile 0; sub-tile s is frag0 ^ (s << 5)
+
+    __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t lane = tid & 63u;
+        const uint32_t k = 2 * wave + (lane >> 5), slot = lane & 31u;
+        krow = k;
+        step = 16 * ld;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t lg = (slot >> 1) ^ fm16(k + 8 * i, kGranules);
+            off[i] = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2;
+        }
+        // ds_read_b64_tr_b16: 16-lane group q reads k rows 32*kk + 8q + 4h + r
+        // (lane 4r + c: columns 4c .. 4c+3 of the 16-column sub-tile); lane i
+        // of the group receives column i.  fm16 sees only k % 4 and bit 3 of k.
+        // Sub-tile granules (wrow / 16 + s) ^ f with wrow / 16 in {0, 8} and
+        // s, f < 8 equal wrow / 16 + (s ^ f), i.e. an XOR of bits 5..7.
+        const uint32_t q = lane >> 4, r = (lane >> 2) & 3u, c = lane & 3u;
+        const uint32_t k0 = 8 * q + r, f = fm16(k0, kGranules);
+        frag0 = k0 * kRowB + c * 8 + (((wrow >> 4) + f) << 5);
+    }
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
+        return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+    }
+    template <bool CHECK>
+    __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
+        const uint32_t m0 = lds + (i * kWaves + wave) * 1024;
+        if (CHECK)
+            dma16(r, k0 + krow + 8 * i < kend ? off[i & 1] + i * step : kOob, m0);
+        else
+            dma16_add(r, off[i & 1], i * step, m0);
+    }
+    template <bool CHECK>
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
+                                          uint32_t kend) const {
+        const u32x4_t r = rsrc(base, bytes, ld, k0);
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
+    }
+    // The stage base is a multiple of 1 KB, so (stage + frag0) ^ (sub << 5)
+    // addresses sub-tile `sub` of that stage.
+    template <int KK>
+    __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
+        constexpr int O0 = KK * 32 * kRowB, O1 = (KK * 32 + 4) * kRowB;
+        const uint32_t a = (stage + frag0) ^ ((uint32_t)sub << 5);
+        short v[8];
+        short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
+        short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
+        lds_load_tr16(a + O0, lo);
+        lds_load_tr16(a + O1, hi);
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+        return __builtin_bit_cast(bf16x8_t, w);
+    }
+};
+
+// v_mfma_f32_16x16x32_bf16 with the accumulator pinned to AGPRs.  Written as
+// asm because the compiler's register allocation of 64 live 16x16 accumulators
+// moves them between VGPRs and AGPRs on every K step.  The compiler does not
+// see an MFMA here, so its wait-state bookkeeping for MFMA results does not
+// apply: the accumulators are only read back by VALU after mfma16_drain().
+__device__ __forceinline__ void mfma16(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Wait states between the last MFMA writing an accumulator and VALU reads of
+// it (8-pass XDL result to VALU read: at most 19), and between VALU writes of
+// accumulators and their first use as MFMA source C.
+__device__ __forceinline__ void mfma16_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+// One 32-wide K step, rows [RB, RE) of SM sub-tile rows, SN MFMAs per row.
+// Next-step fragment reads go to rows [RR, RE): with all rows, A[r] in row r
+// and B two per row; otherwise all reads spread evenly, B first.  DMA
+// instructions [DFIRST, DFIRST + DCOUNT) are spread over the call's rows.
+template <int STEP, int DFIRST, int DCOUNT, bool CHECK, int RB, int RE, int RR, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void mfma16_rows(f32x4_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM], const bf16x8_t (&fb)[SN],
+                                            bf16x8_t (&na)[SM], bf16x8_t (&nb)[SN], const OpA& la, const OpB& lb,
+                                            uint32_t cur, uint32_t nxt, uint32_t fill, u32x4_t ra, u32x4_t rb,
+                                            uint32_t kf, uint32_t kend) {
+    constexpr int NEXT_KK = (STEP + 1) % 2;
+    const uint32_t rd = STEP == 0 ? cur : nxt;
+    constexpr int kRows = RE - RB;
+    constexpr int kPerRow = (DCOUNT + kRows - 1) / kRows;
+    constexpr int kReadRows = RE - RR;
+    constexpr bool kOwn = kReadRows == SM;   // every row reads: A[r] in row r
+    constexpr int kReads = SM + SN;
+    constexpr int kSpread = kReadRows > 0 ? (kReads + kReadRows - 1) / kReadRows : 0;
+#pragma unroll
+    for (int i = RB; i < RE; ++i) {
+        int nbr = 0, nar = 0, bfirst = 0, qfirst = 0;
+        if (i >= RR) {
+            if (kOwn) {
+                bfirst = 2 * (i - RR);
+                const int blast = i == RE - 1 ? SN : bfirst + 2;
+                nbr = (blast < SN ? blast : SN) - (bfirst < SN ? bfirst : SN);
+                nar = 1;
+            } else {
+                qfirst = (i - RR) * kSpread;
+                const int qlast = qfirst + kSpread < kReads ? qfirst + kSpread : kReads;
+                nbr = qlast > qfirst ? qlast - qfirst : 0;   // reads q in [qfirst, qlast): B for q < SN, then A
+            }
+        }
+        const int nr = nbr + nar;
+        const int nitems = kPerRow + nr;
+        const int per_slot = (nitems + SN - 1) / SN;
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            mfma16(acc[i][j], fa[i], fb[j]);
+#pragma unroll
+            for (int u = 0; u < per_slot; ++u) {
+                const int t = j * per_slot + u;
+                if (t < nitems) {
+                    const int it = row_item(t, kPerRow, nr);
+                    if (it >= 256) {
+                        const int rq = it - 256;
+                        if (kOwn) {
+                            if (rq < nbr)
+                                nb[bfirst + rq] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, bfirst + rq);
+                            else
+                                na[i] = la.template read_one<NEXT_KK>(rd, i);
+                        } else {
+                            const int q = qfirst + rq;
+                            if (q < SN)
+                                nb[q] = lb.template read_one<NEXT_KK>(rd + OpA::kStageBytes, q);
+                            else
+                                na[q - SN] = la.template read_one<NEXT_KK>(rd, q - SN);
+                        }
+                    } else {
+                        const int q = DFIRST + (i - RB) * kPerRow + it;
+                        if (q < DFIRST + DCOUNT) {
+                            if (q < OpA::kInstr)
+                                la.template issue_one<CHECK>(q, ra, fill, kf, kend);
+                            else
+                                lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+                        }
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// K loop: two 64 KB stages of 64 K values (two 32-wide steps each).  The DMA
+// of stage s+1 goes out during step 0 of stage s; halfway through step 1 one
+// vmcnt(0)/lgkmcnt(0) wait and a barrier make it visible and free stage s,
+// and the step's second half reads stage s+1's first fragments.
+template <bool CHECK, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
+                                             const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg,
+                                             uint32_t kend, int nst, uint32_t lds0) {
+    bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
+    la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
+    lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
+    T0G_WAIT_VMCNT(0);
+    barrier_no_fence();
+#pragma unroll
+    for (int i = 0; i < SM; ++i) fa0[i] = la.template read_one<0>(lds0, i);
+#pragma unroll
+    for (int j = 0; j < SN; ++j) fb0[j] = lb.template read_one<0>(lds0 + A_BYTES, j);
+
+    constexpr int kHalfRows = SM / 2;
+    uint32_t cur = 0;
+    for (int s = 0; s < nst; ++s) {
+        const uint32_t nxt = cur ^ STAGE;
+        const uint32_t kf = kbeg + (uint32_t)(s + 1) * 64;
+        const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+        const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+        mfma16_rows<0, 0, kVmemPerStage, CHECK, 0, SM, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt,
+                                                         lds0 + nxt, ra, rb, kf, kend);
+        mfma16_rows<1, 0, 0, CHECK, 0, kHalfRows, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt,
+                                                            lds0 + nxt, ra, rb, kf, kend);
+        __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+        barrier_no_fence();
+        mfma16_rows<1, 0, 0, CHECK, kHalfRows, SM, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                             lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
+        cur = nxt;
+    }
+}
+
+// Epilogue: each wave stages 32 rows x WTN columns of fp32 at a time through
+// its own LDS region, rows padded to WTN + 4 words (the 16x16 result puts the
+// four lane groups 4 rows apart; a 4-row step of 132 words moves 16 banks), and
+// writes whole rows with 16-byte stores.
+template <int SN>
+struct VecEpilogue16 {
+    static constexpr int kWTN = SN * 16;
+    static constexpr uint32_t kStride = (kWTN + 4) * 4;
+    static constexpr uint32_t kWaveBytes = 32 * kStride;
+};
+
+template <int SM, int SN, bool OUT_BF16>
+__device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32x4_t (&acc)[SM][SN], uint32_t row0,
+                                                 uint32_t col0, uint32_t lane, uint32_t lds, bool vec) {
+    typedef VecEpilogue16<SN> E;
+    typedef __attribute__((address_space(3))) float lds_f32;
+    typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
+    constexpr int kCols = OUT_BF16 ? 8 : 4;
+    constexpr int kLanesPerRow = E::kWTN / kCols;
+    constexpr int kRowsPerPass = 64 / kLanesPerRow;
+    static_assert(kLanesPerRow <= 64 && 64 % kLanesPerRow == 0, "row must map onto whole lanes");
+    static_assert(SM % 2 == 0, "32-row staging blocks");
+    const uint32_t l16 = lane & 15u, q = lane >> 4;
+    const uint32_t rl = lane / kLanesPerRow, cl = (lane % kLanesPerRow) * kCols;
+    float bv[kCols];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
+    if (p.epilogue != 0) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
+#pragma unroll
+        for (int c = 0; c < kCols; ++c)
+            bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + cl + c) * 4u, 0, 0));
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    }
+    const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+    const uint32_t esize = OUT_BF16 ? 2u : 4u;
+#pragma unroll
+    for (int i2 = 0; i2 < SM; i2 += 2) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = 16 * ii + 4 * q + r;
+                    *reinterpret_cast<lds_f32*>((uintptr_t)(lds + row * E::kStride + (j * 16 + l16) * 4)) =
+                        acc[i2 + ii][j][r];
+                }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int pass = 0; pass < 32 / kRowsPerPass; ++pass) {
+            const uint32_t rr = pass * kRowsPerPass + rl;
+            float v[kCols];
+#pragma unroll
+            for (int c = 0; c < kCols; c += 4) {
+                const f32x4_t qv = *reinterpret_cast<const lds_f32x4*>((uintptr_t)(lds + rr * E::kStride + (cl + c) * 4));
+                v[c] = qv[0];
+                v[c + 1] = qv[1];
+                v[c + 2] = qv[2];
+                v[c + 3] = qv[3];
+            }
+#pragma unroll
+            for (int c = 0; c < kCols; ++c) v[c] = apply_epilogue(v[c], bv[c], p.epilogue);
+            const uint32_t grow = row0 + i2 * 16 + rr, gcol = col0 + cl;
+            const uint64_t addr = cbase + ((uint64_t)grow * p.ldc + gcol) * esize;
+            if (vec) {
+                u32x4_t w;
+                if constexpr (OUT_BF16) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const __bf16 lo = (__bf16)v[2 * c], hi = (__bf16)v[2 * c + 1];
+                        w[c] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) w[c] = __builtin_bit_cast(uint32_t, v[c]);
+                }
+                __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
+            } else if (grow < p.m) {
+#pragma unroll
+                for (int c = 0; c < kCols; ++c) {
+                    if (gcol + c < p.n) {
+                        if constexpr (OUT_BF16)
+                            reinterpret_cast<gbf16_t*>((uintptr_t)addr)[c] = (__bf16)v[c];
+                        else
+                            reinterpret_cast<gf32_t*>((uintptr_t)addr)[c] = v[c];
+                    }
+                }
+            }
+        }
+        asm volatile("" ::: "memory");
+    }
+}
+
+// The 256x256 fast path on 16x16x32 MFMAs (2 x 2 waves of 128 x 128).
+template <bool A_K, bool B_K, bool OUT_BF16>
+__device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
+    constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 2;
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int SM = WTM / 16, SN = WTN / 16;
+    using OpA = Op16<A_K, BM, NT, SM>;
+    using OpB = Op16<B_K, BN, NT, SN>;
+    constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
+    constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+    const uint32_t tid = threadIdx.x;
+    uint32_t bid = blockIdx.x;
+    const uint32_t nblk = p.tiles_m * p.tiles_n;
+    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    const uint32_t gm = p.group_m;
+    const uint32_t per_group = gm * p.tiles_n;
+    const uint32_t group = bid / per_group;
+    const uint32_t first_m = group * gm;
+    const uint32_t gsz = min(p.tiles_m - first_m, gm);
+    const uint32_t in_group = bid - group * per_group;
+    const uint32_t m0 = (first_m + in_group % gsz) * BM;
+    const uint32_t n0 = (in_group / gsz) * BN;
+
+    const uint32_t kbeg = blockIdx.y * p.k_per_split;
+    const uint32_t kend = min(p.k, kbeg + p.k_per_split);
+    const int nst = kend > kbeg ? (int)((kend - kbeg + 63) / 64) : 0;
+
+    const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+    const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+    OpA la;
+    OpB lb;
+    la.init(tid, m0, p.lda, wm * WTM);
+    lb.init(tid, n0, p.ldb, wn * WTN);
+
+    f32x4_t acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = f32x4_t{};
+
+    if (nst > 0) {
+        mfma16_drain();
+        const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+        if ((kend - kbeg) % 64 == 0)
+            k_pipeline16<false, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0);
+        else
+            k_pipeline16<true, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0);
+    }
+
+    static_assert((NT / 64) * VecEpilogue16<SN>::kWaveBytes <= 2 * STAGE, "epilogue staging must fit the stages");
+    mfma16_drain();
+    T0G_WAIT_VMCNT(0);
+    barrier_no_fence();
+    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+    store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                       lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+}
+
+}  // namespace t0g
+
+#endif

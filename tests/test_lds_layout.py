@@ -156,3 +156,104 @@ def test_fragment_reads_are_bank_conflict_free(rows, bk):
                     k = kk * 16 + 8 * g + r
                     addrs.append((k * row_bytes + (((2 * sub + gp) ^ fm(k, granules)) << 5) + q * 8, 8))
                 assert _banks(addrs, 256) == 1
+
+
+# ---- 16x16x32 MFMA fragments (256x256 tile, 64 K values per stage) ----------
+# Lane (l16 = lane % 16, q = lane // 16) of K step kk (32 wide) needs row (or
+# column) l16 of its 16-wide sub-tile and k = 32*kk + 8*q + e, e = 0..7.
+def fm16(k, granules):
+    return (((0x7520 >> ((k & 3) * 4)) & 0xF) ^ ((k >> 3) & 1)) & (granules - 1)
+
+
+def dma_mnmajor16(rows, waves, bk=64):
+    lds = {}
+    row_bytes = rows * 2
+    granules = rows // 16
+    instr = bk * row_bytes // 1024 // waves
+    for wave in range(waves):
+        for i in range(instr):
+            base = (i * waves + wave) * 1024
+            for lane in range(64):
+                pos = base + lane * 16
+                k = pos // row_bytes
+                slot = (pos % row_bytes) // 16
+                lg = (slot >> 1) ^ fm16(k, granules)
+                for e in range(8):
+                    lds[pos + 2 * e] = (lg * 16 + (slot & 1) * 8 + e, k)
+    return lds
+
+
+def frag16_kmajor(lds, wrow, sub, kk, bk=64):
+    out = {}
+    for lane in range(64):
+        l16, q = lane & 15, lane >> 4
+        row = wrow + l16
+        addr = row * bk * 2 + sub * 16 * bk * 2 + (((4 * kk + q) ^ fk(row, bk)) << 4)
+        out[lane] = [lds[addr + 2 * e] for e in range(8)]
+    return out
+
+
+def frag16_mnmajor_addrs(rows, wcol, sub, kk, h):
+    row_bytes = rows * 2
+    granules = rows // 16
+    addr = {}
+    for lane in range(64):
+        q, r, c = lane >> 4, (lane >> 2) & 3, lane & 3
+        k = 32 * kk + 8 * q + 4 * h + r
+        gi = (wcol >> 4) + sub
+        addr[lane] = k * row_bytes + ((gi ^ fm16(k, granules)) << 5) + c * 8
+    return addr
+
+
+def frag16_mnmajor(lds, rows, wcol, sub, kk):
+    a = [frag16_mnmajor_addrs(rows, wcol, sub, kk, h) for h in range(2)]
+    out = {}
+    for lane in range(64):
+        grp, i = lane // 16, lane % 16
+        vals = []
+        for h in range(2):
+            for r in range(4):
+                src = 16 * grp + 4 * r + i // 4
+                vals.append(lds[a[h][src] + 2 * (i % 4)])
+        out[lane] = vals
+    return out
+
+
+def expected16(wrow, sub, kk):
+    return {lane: [(wrow + sub * 16 + (lane & 15), 32 * kk + 8 * (lane >> 4) + e) for e in range(8)]
+            for lane in range(64)}
+
+
+def test_mfma16_kmajor_fragments():
+    lds = dma_kmajor(256, 4, 64)
+    for wrow in (0, 128):
+        for sub in range(8):
+            for kk in range(2):
+                assert frag16_kmajor(lds, wrow, sub, kk) == expected16(wrow, sub, kk)
+
+
+def test_mfma16_mnmajor_fragments():
+    lds = dma_mnmajor16(256, 4, 64)
+    assert len(lds) == 256 * 64
+    for wcol in (0, 128):
+        for sub in range(8):
+            for kk in range(2):
+                assert frag16_mnmajor(lds, 256, wcol, sub, kk) == expected16(wcol, sub, kk)
+
+
+def test_mfma16_reads_are_bank_conflict_free():
+    # ds_read_b128 (K-contiguous): 16-lane phases
+    for lane0 in range(0, 64, 16):
+        for kk in range(2):
+            addrs = []
+            for lane in range(lane0, lane0 + 16):
+                row = lane & 15
+                addrs.append((row * 128 + (((4 * kk + (lane >> 4)) ^ fk(row, 64)) << 4), 16))
+            assert _banks(addrs, 256) == 1
+    # ds_read_b64_tr_b16 (M/N-contiguous): 32-lane phases
+    for sub in range(8):
+        for kk in range(2):
+            for h in range(2):
+                a = frag16_mnmajor_addrs(256, 0, sub, kk, h)
+                for half in range(2):
+                    assert _banks([(a[l], 8) for l in range(32 * half, 32 * half + 32)], 256) == 1
