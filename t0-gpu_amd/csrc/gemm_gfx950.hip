@@ -30,6 +30,9 @@
 #ifndef T0G_MFMA16
 #define T0G_MFMA16 1
 #endif
+#ifndef T0G_PINGPONG
+#define T0G_PINGPONG 1
+#endif
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // Global-memory pointer types: with an explicit address space the compiler
@@ -1043,7 +1046,11 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 // 256x256 tiles hold 256 fp32 accumulators per lane: one wave per SIMD, the
 // whole 512-entry VGPR+AGPR file.  Smaller tiles leave room for two workgroups
 // per CU (LDS 64 KB or less each).
+#if T0G_PINGPONG
+#define T0G_WPE_256x256 2, 2
+#else
 #define T0G_WPE_256x256 1, 1
+#endif
 #define T0G_WPE_128x128 1, 2
 #define T0G_WPE_64x64 1, 4
 // Fast-path pipeline (K values per stage, stages): 256x256 double-buffers
@@ -1055,7 +1062,9 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 #define T0G_GEMM(NAME, BM, BN, WM, WN, AK, BKM, OBF, AL)                                       \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                   \
         __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmArgs p) {          \
-        if constexpr (AL && BM == 256 && T0G_MFMA16)                                             \
+        if constexpr (AL && BM == 256 && T0G_PINGPONG)                                           \
+            t0g::gemm_tile_pp<AK, BKM, OBF>(p);                                                  \
+        else if constexpr (AL && BM == 256 && T0G_MFMA16)                                        \
             t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                              \
         else if constexpr (AL)                                                                   \
             t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_##BM##x##BN>(p);            \
@@ -1096,7 +1105,11 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, f32, false)     \
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, bf16, true)
 
+#if T0G_PINGPONG
+T0G_GEMM_TILE(t0g_gemm_256x256_k64, 256, 256, 2, 4)
+#else
 T0G_GEMM_TILE(t0g_gemm_256x256_k64, 256, 256, 2, 2)
+#endif
 T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)

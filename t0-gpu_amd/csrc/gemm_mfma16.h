@@ -45,18 +45,19 @@ struct Op16;
 
 // K-contiguous operand of a 256-row tile, 64 K values per stage: 128-byte LDS
 // rows, chunk swizzle fk<64>.  DMA instruction i of a wave covers rows
-// 32 i + 8 wave + lane / 8; fk<64> of those rows does not depend on i, so one
-// offset register and one K column serve all of a wave's instructions.
+// 8 (i W + wave) + lane / 8 (W waves); for even W, fk<64> of those rows does not
+// depend on i, so one offset register and one K column serve all of a wave's
+// instructions.
 template <int ROWS, int NT, int SUBS>
 struct Op16<true, ROWS, NT, SUBS> {
     static constexpr int kWaves = NT / 64;
     static constexpr uint32_t kKRow = 128;
     static constexpr int kInstr = ROWS * kKRow / 1024 / kWaves;
-    static_assert(ROWS == 256 && kWaves == 4, "offset sharing assumes a 256-row tile and 4 waves");
+    static_assert(ROWS == 256 && (kWaves == 4 || kWaves == 8), "offset sharing assumes a 256-row tile, 4 or 8 waves");
     static constexpr uint32_t kStageBytes = ROWS * kKRow;
     uint32_t off0;    // byte offset of instruction 0's piece at k = 0
     uint32_t kcol;    // first K column of the lane's piece
-    uint32_t step;    // bytes between instructions (32 rows)
+    uint32_t step;    // bytes between instructions (8 W rows)
     uint32_t wave;
     uint32_t frag[2];   // per 32-wide K step: LDS offset of the lane's chunk in sub-tile 0
 
@@ -67,7 +68,7 @@ struct Op16<true, ROWS, NT, SUBS> {
         const uint32_t c = (lane & 7u) ^ fk<64>(r);
         kcol = c * 8;
         off0 = ((row0 + r) * ld + c * 8) * 2;
-        step = 64 * ld;
+        step = 16 * kWaves * ld;
         const uint32_t row = wrow + (lane & 15u), qk = lane >> 4;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) frag[kk] = row * kKRow + (((4u * kk + qk) ^ fk<64>(row)) << 4);
@@ -99,8 +100,9 @@ struct Op16<true, ROWS, NT, SUBS> {
 
 // M/N-contiguous operand of a 256-column tile: LDS rows are k rows of 512
 // bytes, granule swizzle fm16.  DMA instruction i of a wave covers k rows
-// 8 i + 2 wave + lane / 32; their swizzle differs only by bit 0 of i, so two
-// offset registers serve all of a wave's instructions.
+// 2 (i W + wave) + lane / 32 (W waves); their swizzle depends on i only through
+// bit 0 of i (W = 4) or not at all (W = 8), so two offset registers serve all
+// of a wave's instructions.
 template <int ROWS, int NT, int SUBS>
 struct Op16<false, ROWS, NT, SUBS> {
     static constexpr int kWaves = NT / 64;
@@ -108,10 +110,11 @@ struct Op16<false, ROWS, NT, SUBS> {
     static constexpr uint32_t kGranules = ROWS / 16;
     static constexpr uint32_t kStageBytes = 64 * kRowB;
     static constexpr int kInstr = kStageBytes / 1024 / kWaves;
-    static_assert(ROWS == 256 && kWaves == 4, "offset sharing assumes a 256-column tile and 4 waves");
+    static_assert(ROWS == 256 && (kWaves == 4 || kWaves == 8), "offset sharing assumes a 256-column tile, 4 or 8 waves");
+    static_assert(SUBS == 4 || SUBS == 8, "sub-tile granules are XORed into a 4- or 8-aligned base");
     uint32_t off[2];   // byte offsets of instructions 0 and 1 (less one instruction step) at k = 0
     uint32_t krow;     // k row of instruction 0's piece
-    uint32_t step;     // bytes between instructions (8 k rows)
+    uint32_t step;     // bytes between instructions (2 W k rows)
     uint32_t wave;
     uint32_t frag0;    // K step 0, half 0, sub-tile 0; sub-tile s is frag0 ^ (s << 5)
 
@@ -120,20 +123,20 @@ struct Op16<false, ROWS, NT, SUBS> {
         const uint32_t lane = tid & 63u;
         const uint32_t k = 2 * wave + (lane >> 5), slot = lane & 31u;
         krow = k;
-        step = 16 * ld;
+        step = 4 * kWaves * ld;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const uint32_t lg = (slot >> 1) ^ fm16(k + 8 * i, kGranules);
+            const uint32_t lg = (slot >> 1) ^ fm16(k + 2 * kWaves * i, kGranules);
             off[i] = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2;
         }
         // ds_read_b64_tr_b16: 16-lane group q reads k rows 32*kk + 8q + 4h + r
         // (lane 4r + c: columns 4c .. 4c+3 of the 16-column sub-tile); lane i
         // of the group receives column i.  fm16 sees only k % 4 and bit 3 of k.
-        // Sub-tile granules (wrow / 16 + s) ^ f with wrow / 16 in {0, 8} and
-        // s, f < 8 equal wrow / 16 + (s ^ f), i.e. an XOR of bits 5..7.
+        // Sub-tile granule (wrow / 16 + s) ^ f, with wrow / 16 a multiple of
+        // SUBS and s < SUBS, equals (wrow / 16 ^ f) ^ s: an XOR of bits 5 and up.
         const uint32_t q = lane >> 4, r = (lane >> 2) & 3u, c = lane & 3u;
         const uint32_t k0 = 8 * q + r, f = fm16(k0, kGranules);
-        frag0 = k0 * kRowB + c * 8 + (((wrow >> 4) + f) << 5);
+        frag0 = k0 * kRowB + c * 8 + (((wrow >> 4) ^ f) << 5);
     }
     __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
         return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
@@ -142,7 +145,7 @@ struct Op16<false, ROWS, NT, SUBS> {
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
         const uint32_t m0 = lds + (i * kWaves + wave) * 1024;
         if (CHECK)
-            dma16(r, k0 + krow + 8 * i < kend ? off[i & 1] + i * step : kOob, m0);
+            dma16(r, k0 + krow + 2 * kWaves * i < kend ? off[i & 1] + i * step : kOob, m0);
         else
             dma16_add(r, off[i & 1], i * step, m0);
     }
@@ -257,18 +260,28 @@ __device__ __forceinline__ void mfma16_rows(f32x4_t (&acc)[SM][SN], const bf16x8
     }
 }
 
-// K loop: two 64 KB stages of 64 K values (two 32-wide steps each).  The DMA
-// of stage s+1 goes out during step 0 of stage s; halfway through step 1 one
-// vmcnt(0)/lgkmcnt(0) wait and a barrier make it visible and free stage s,
-// and the step's second half reads stage s+1's first fragments.
+// K loop: two 64 KB stages of 64 K values (two 32-wide steps each).  Halfway
+// through step 1 of stage s one vmcnt(0)/lgkmcnt(0) wait and a barrier make
+// stage s + 1 visible and free the buffer of stage s; the step's second half
+// reads stage s + 1's first fragments and starts the DMA of stage s + 2 into
+// the freed buffer (the A half), whose B half follows during step 0 of stage
+// s + 1.  Each DMA so has half a stage or more to land before it is waited on.
+// Stages past the end get an empty descriptor: their DMA writes zeros to LDS
+// and reads no memory.
 template <bool CHECK, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
                                              const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg,
                                              uint32_t kend, int nst, uint32_t lds0) {
+    constexpr int kHalf = OpA::kInstr;   // the A half of a stage's DMA, then the B half
+    static_assert(OpA::kInstr == OpB::kInstr, "equal A and B halves");
     bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
     la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
     lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
-    T0G_WAIT_VMCNT(0);
+    {
+        const uint32_t k1 = kbeg + 64;
+        la.template issue<CHECK>(lds0 + STAGE, p.a, k1 < kend ? a_bytes : 0u, p.lda, k1, kend);
+    }
+    T0G_WAIT_VMCNT(kHalf);
     barrier_no_fence();
 #pragma unroll
     for (int i = 0; i < SM; ++i) fa0[i] = la.template read_one<0>(lds0, i);
@@ -279,17 +292,17 @@ __device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& 
     uint32_t cur = 0;
     for (int s = 0; s < nst; ++s) {
         const uint32_t nxt = cur ^ STAGE;
-        const uint32_t kf = kbeg + (uint32_t)(s + 1) * 64;
-        const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
-        const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-        mfma16_rows<0, 0, kVmemPerStage, CHECK, 0, SM, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt,
-                                                         lds0 + nxt, ra, rb, kf, kend);
+        const uint32_t k1 = kbeg + (uint32_t)(s + 1) * 64, k2 = k1 + 64;
+        const u32x4_t rb1 = lb.rsrc(p.b, k1 < kend ? b_bytes : 0u, p.ldb, k1);
+        const u32x4_t ra2 = la.rsrc(p.a, k2 < kend ? a_bytes : 0u, p.lda, k2);
+        mfma16_rows<0, kHalf, kHalf, CHECK, 0, SM, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt,
+                                                     lds0 + nxt, ra2, rb1, k1, kend);
         mfma16_rows<1, 0, 0, CHECK, 0, kHalfRows, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt,
-                                                            lds0 + nxt, ra, rb, kf, kend);
+                                                            lds0 + nxt, ra2, rb1, k1, kend);
         __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
         barrier_no_fence();
-        mfma16_rows<1, 0, 0, CHECK, kHalfRows, SM, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                             lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
+        mfma16_rows<1, 0, kHalf, CHECK, kHalfRows, SM, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
+                                                                 lds0 + nxt, lds0 + cur, ra2, rb1, k2, kend);
         cur = nxt;
     }
 }
@@ -390,6 +403,23 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
     }
 }
 
+// Output tile of this workgroup: block ids remapped so each XCD (own L2) works
+// on a contiguous patch, walked in groups of group_m tile rows.
+template <int BM, int BN>
+__device__ __forceinline__ void tile_origin(const T0gGemmArgs& p, uint32_t& m0, uint32_t& n0) {
+    uint32_t bid = blockIdx.x;
+    const uint32_t nblk = p.tiles_m * p.tiles_n;
+    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    const uint32_t gm = p.group_m;
+    const uint32_t per_group = gm * p.tiles_n;
+    const uint32_t group = bid / per_group;
+    const uint32_t first_m = group * gm;
+    const uint32_t gsz = min(p.tiles_m - first_m, gm);
+    const uint32_t in_group = bid - group * per_group;
+    m0 = (first_m + in_group % gsz) * BM;
+    n0 = (in_group / gsz) * BN;
+}
+
 // The 256x256 fast path on 16x16x32 MFMAs (2 x 2 waves of 128 x 128).
 template <bool A_K, bool B_K, bool OUT_BF16>
 __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
@@ -404,17 +434,8 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
     const uint32_t tid = threadIdx.x;
-    uint32_t bid = blockIdx.x;
-    const uint32_t nblk = p.tiles_m * p.tiles_n;
-    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
-    const uint32_t gm = p.group_m;
-    const uint32_t per_group = gm * p.tiles_n;
-    const uint32_t group = bid / per_group;
-    const uint32_t first_m = group * gm;
-    const uint32_t gsz = min(p.tiles_m - first_m, gm);
-    const uint32_t in_group = bid - group * per_group;
-    const uint32_t m0 = (first_m + in_group % gsz) * BM;
-    const uint32_t n0 = (in_group / gsz) * BN;
+    uint32_t m0, n0;
+    tile_origin<BM, BN>(p, m0, n0);
 
     const uint32_t kbeg = blockIdx.y * p.k_per_split;
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
@@ -443,6 +464,133 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
             k_pipeline16<false, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0);
         else
             k_pipeline16<true, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0);
+    }
+
+    static_assert((NT / 64) * VecEpilogue16<SN>::kWaveBytes <= 2 * STAGE, "epilogue staging must fit the stages");
+    mfma16_drain();
+    T0G_WAIT_VMCNT(0);
+    barrier_no_fence();
+    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+    store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                       lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+}
+
+
+// Ping-pong pipeline of the 8-wave 256x256 kernel.  Waves 0-3 (group 0) and
+// 4-7 (group 1) share the four SIMDs, one of each per SIMD, and alternate
+// between a load phase (fragment reads, DMA issue, waits) and a compute phase
+// (32 MFMAs and nothing else), offset by one phase: while one wave of a SIMD
+// multiplies, the other one feeds LDS and its registers.  A wave's VMEM
+// instruction holds up its own next MFMA for a good part of the texture
+// unit's 16 cycles per 1 KB request; here that time falls on the other wave's
+// MFMAs.  Every phase ends at a workgroup barrier; group 1 starts one barrier
+// late and group 0 ends one barrier late.
+//
+// Stage s (64 K values) spans four phases: 4s (group 0 loads step 0), 4s + 1
+// (group 1 loads step 0), 4s + 2 and 4s + 3 (step 1).  The DMA of stage s + 1
+// goes into the buffer of stage s - 1, free since the barrier closing phase
+// 4s - 1, and must be complete at the barrier closing phase 4s + 3.  Group 1
+// sends its share in phase 4s + 1 and retires it in phase 4s + 3; group 0
+// sends its A share in phase 4s and its B share in phase 4s + 2 and retires
+// both at the end of its compute phase 4s + 3, so no phase carries more than
+// half of the CU's DMA requests for the stage.
+template <bool CHECK, uint32_t A_BYTES, uint32_t STAGE, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void k_pipeline_pp(f32x4_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
+                                              const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes,
+                                              uint32_t kbeg, uint32_t kend, int nst, uint32_t lds0, uint32_t group) {
+    bf16x8_t fa[SM], fb[SN];
+    la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
+    lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
+    T0G_WAIT_VMCNT(0);
+    barrier_no_fence();
+    if (group != 0) barrier_no_fence();
+    for (int s = 0; s < nst; ++s) {
+        const uint32_t cur = lds0 + ((s & 1) ? STAGE : 0u), nxt = lds0 + ((s & 1) ? 0u : STAGE);
+        // load phase, K step 0: fragment reads first, so their latency runs
+        // while the DMA issues
+#pragma unroll
+        for (int i = 0; i < SM; ++i) fa[i] = la.template read_one<0>(cur, i);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) fb[j] = lb.template read_one<0>(cur + A_BYTES, j);
+        asm volatile("" ::: "memory");
+        if (s + 1 < nst) {
+            const uint32_t k1 = kbeg + (uint32_t)(s + 1) * 64;
+            la.template issue<CHECK>(nxt, p.a, a_bytes, p.lda, k1, kend);
+            if (group != 0) lb.template issue<CHECK>(nxt + A_BYTES, p.b, b_bytes, p.ldb, k1, kend);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        barrier_no_fence();
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) mfma16(acc[i][j], fa[i], fb[j]);
+        barrier_no_fence();
+        // load phase, K step 1
+#pragma unroll
+        for (int i = 0; i < SM; ++i) fa[i] = la.template read_one<1>(cur, i);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) fb[j] = lb.template read_one<1>(cur + A_BYTES, j);
+        if (group == 0) {
+            asm volatile("" ::: "memory");
+            if (s + 1 < nst) lb.template issue<CHECK>(nxt + A_BYTES, p.b, b_bytes, p.ldb, kbeg + (uint32_t)(s + 1) * 64, kend);
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+        }
+        barrier_no_fence();
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) mfma16(acc[i][j], fa[i], fb[j]);
+        if (group == 0) T0G_WAIT_VMCNT(0);
+        barrier_no_fence();
+    }
+    if (group == 0) barrier_no_fence();
+}
+
+// The 256x256 tile with 8 waves (2 x 4 of 128 x 64) in ping-pong: two waves per
+// SIMD, 128 accumulators each.
+template <bool A_K, bool B_K, bool OUT_BF16>
+__device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
+    constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4;
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int SM = WTM / 16, SN = WTN / 16;
+    using OpA = Op16<A_K, BM, NT, SM>;
+    using OpB = Op16<B_K, BN, NT, SN>;
+    constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+    const uint32_t tid = threadIdx.x;
+    uint32_t m0, n0;
+    tile_origin<BM, BN>(p, m0, n0);
+    const uint32_t kbeg = blockIdx.y * p.k_per_split;
+    const uint32_t kend = min(p.k, kbeg + p.k_per_split);
+    const int nst = kend > kbeg ? (int)((kend - kbeg + 63) / 64) : 0;
+    const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+    const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+
+    const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+    OpA la;
+    OpB lb;
+    la.init(tid, m0, p.lda, wm * WTM);
+    lb.init(tid, n0, p.ldb, wn * WTN);
+
+    f32x4_t acc[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) acc[i][j] = f32x4_t{};
+
+    if (nst > 0) {
+        mfma16_drain();
+        const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+        const uint32_t group = wave >> 2;
+        if ((kend - kbeg) % 64 == 0)
+            k_pipeline_pp<false, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0, group);
+        else
+            k_pipeline_pp<true, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0, group);
     }
 
     static_assert((NT / 64) * VecEpilogue16<SN>::kWaveBytes <= 2 * STAGE, "epilogue staging must fit the stages");

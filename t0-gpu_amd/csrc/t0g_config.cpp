@@ -37,8 +37,9 @@ int ok() {
 // workgroups = t0_us + (per-CU FLOP) / rate, linear in K to within a few
 // percent over K = 256 .. 8192.  64x64 gains throughput from co-resident
 // workgroups, 128x128 does not (one already saturates the CU's LDS traffic).
+// 256x256 runs 8 waves (two per SIMD, in ping-pong).
 const TileDef kTiles[kNumTiles] = {
-    {256, 256, 256, 1, 13.9, 5243.0, 5243.0, "t0g_gemm_256x256_k64"},
+    {256, 256, 512, 1, 13.9, 5243.0, 5243.0, "t0g_gemm_256x256_k64"},
     {128, 128, 256, 2, 6.7, 3034.0, 3034.0, "t0g_gemm_128x128_k64"},
     {64, 64, 256, 4, 2.6, 931.0, 1606.0, "t0g_gemm_64x64_k64"},
 };

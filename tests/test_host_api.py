@@ -43,13 +43,13 @@ def test_version_and_last_error():
     assert "unknown preset" in t0g.last_error()
 
 
-@pytest.mark.parametrize("name,bm,bn", [("tile_256x256_k64", 256, 256), ("tile_128x128_k64", 128, 128),
-                                        ("tile_64x64_k64", 64, 64)])
-def test_presets_and_derived_fields(name, bm, bn):
+@pytest.mark.parametrize("name,bm,bn,wg", [("tile_256x256_k64", 256, 256, 512), ("tile_128x128_k64", 128, 128, 256),
+                                           ("tile_64x64_k64", 64, 64, 256)])
+def test_presets_and_derived_fields(name, bm, bn, wg):
     c = t0g.GemmConfig.preset(name)
     c.validate()
-    assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size) == (bm, bn, 64, 256)
-    assert c.n_waves() == 4                        # wave64
+    assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size) == (bm, bn, 64, wg)
+    assert c.n_waves() == wg // 64                 # wave64
     assert c.lds_total() == 2 * (bm + bn) * 64 * 2  # lds_total: 2 buffers x (X + WT) tiles
     assert c.name() == f"t0_gemm_{bm}x{bn}_k64_ldsdb"
     assert c.copy(split_k=4).name() == f"t0_gemm_{bm}x{bn}_k64_ldsdb_sk4"

@@ -257,3 +257,70 @@ def test_mfma16_reads_are_bank_conflict_free():
                 a = frag16_mnmajor_addrs(256, 0, sub, kk, h)
                 for half in range(2):
                     assert _banks([(a[l], 8) for l in range(32 * half, 32 * half + 32)], 256) == 1
+
+
+# ---- kernel address formulas of the 16x16 operands, 4 and 8 waves -----------
+def dma_kmajor16_kernel(waves):
+    """LDS byte -> (row, k) as the K-major 16x16 operand issues its DMA:
+    one offset register per wave, instruction i adds 8*waves rows."""
+    lds = {}
+    for wave in range(waves):
+        for lane in range(64):
+            r0 = 8 * wave + (lane >> 3)
+            c = (lane & 7) ^ fk(r0, 64)
+            for i in range(256 * 128 // 1024 // waves):
+                r = r0 + 8 * waves * i
+                assert fk(r, 64) == fk(r0, 64)          # one K column per lane
+                m0 = (i * waves + wave) * 1024
+                for e in range(8):
+                    lds[m0 + lane * 16 + 2 * e] = (r, c * 8 + e)
+    return lds
+
+
+def dma_mnmajor16_kernel(waves):
+    """Same for the M/N-major operand: two offset registers (i even / odd)."""
+    lds = {}
+    for wave in range(waves):
+        for lane in range(64):
+            k0, slot = 2 * wave + (lane >> 5), lane & 31
+            lg = [(slot >> 1) ^ fm16(k0 + 2 * waves * j, 16) for j in range(2)]
+            for i in range(64 * 512 // 1024 // waves):
+                k = k0 + 2 * waves * i
+                assert (slot >> 1) ^ fm16(k, 16) == lg[i & 1]
+                m0 = (i * waves + wave) * 1024
+                for e in range(8):
+                    lds[m0 + lane * 16 + 2 * e] = (lg[i & 1] * 16 + (slot & 1) * 8 + e, k)
+    return lds
+
+
+def frag16_mnmajor_kernel(lds, wcol, sub, kk, stage=0):
+    """ds_read_b64_tr_b16 addresses as the kernel forms them: (stage + frag0) ^ (sub << 5)."""
+    a = [{}, {}]
+    for lane in range(64):
+        q, r, c = lane >> 4, (lane >> 2) & 3, lane & 3
+        k0 = 8 * q + r
+        frag0 = k0 * 512 + c * 8 + (((wcol >> 4) ^ fm16(k0, 16)) << 5)
+        base = (stage + frag0) ^ (sub << 5)
+        for h in range(2):
+            a[h][lane] = base + (32 * kk + 4 * h) * 512 - stage
+    out = {}
+    for lane in range(64):
+        grp, i = lane // 16, lane % 16
+        out[lane] = [lds[a[h][16 * grp + 4 * r + i // 4] + 2 * (i % 4)] for h in range(2) for r in range(4)]
+    return out
+
+
+@pytest.mark.parametrize("waves", [4, 8])
+def test_mfma16_kernel_dma_matches_layout(waves):
+    assert dma_kmajor16_kernel(waves) == dma_kmajor(256, waves, 64)
+    assert dma_mnmajor16_kernel(waves) == dma_mnmajor16(256, waves, 64)
+
+
+@pytest.mark.parametrize("waves,wtn", [(4, 128), (8, 64)])
+def test_mfma16_kernel_mnmajor_fragments(waves, wtn):
+    lds = dma_mnmajor16_kernel(waves)
+    for wcol in range(0, 256, wtn):
+        for sub in range(wtn // 16):
+            for kk in range(2):
+                for stage in (0, 65536):
+                    assert frag16_mnmajor_kernel(lds, wcol, sub, kk, stage) == expected16(wcol, sub, kk)
