@@ -27,12 +27,6 @@
 
 #include "t0g_kernel_args.h"
 
-#ifndef T0G_MFMA16
-#define T0G_MFMA16 1
-#endif
-#ifndef T0G_PINGPONG
-#define T0G_PINGPONG 1
-#endif
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // Global-memory pointer types: with an explicit address space the compiler
@@ -817,18 +811,16 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
     }
 }
 
-// The K loop of the fast path.  BK 32: ring of NS >= 4 stages, DMA NS-1
-// stages ahead, one barrier per stage.  BK 64: NS = 2 (double buffer): the DMA
-// of stage s+1 is issued during the first half of stage s and retired, with one
-// barrier, halfway through the stage's last K step, before its second half reads
-// stage s+1's first fragments.
+// The K loop of the fast path (128x128 and 64x64 tiles): ring of NS >= 4
+// stages of BK 32, DMA NS-1 stages ahead, one barrier per stage.
 template <bool CHECK, uint32_t BK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN,
           class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& la, const OpB& lb, const T0gGemmArgs& p,
                                            uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg, uint32_t kend, int nst,
                                            uint32_t lds0) {
+    static_assert(BK == 32 && NS >= 4, "ring of BK 32 stages");
     bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
-    if constexpr (BK == 32) {
+    {
         // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
 #pragma unroll
         for (int s = 0; s < NS - 1; ++s) {
@@ -859,40 +851,6 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
             fill = cur;
             cur = nxt;
         }
-    } else {
-        static_assert(BK == 64 && NS == 2, "BK 64 double-buffers");
-        la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
-        lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
-        T0G_WAIT_VMCNT(0);
-        barrier_no_fence();
-        la.template read<0>(lds0, fa0);
-        lb.template read<0>(lds0 + A_BYTES, fb0);
-
-        constexpr int kHalf = (kVmemPerStage + 1) / 2;
-        uint32_t cur = 0;
-        for (int s = 0; s < nst; ++s) {
-            const uint32_t nxt = cur ^ STAGE;   // the other buffer, freed by the previous barrier
-            const uint32_t kf = kbeg + (uint32_t)(s + 1) * BK;
-            const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
-            const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-            mfma_rows<0, 4, 0, kHalf, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
-                                             ra, rb, kf, kend);
-            mfma_rows<1, 4, kHalf, kVmemPerStage - kHalf, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                                 lds0 + nxt, lds0 + nxt, ra, rb, kf, kend);
-            mfma_rows<2, 4, 0, 0, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt, ra, rb,
-                                         kf, kend);
-            // Rows 0-1 of the last step need no new data, which gives the DMA
-            // half a step more.  Then stage s+1 must have landed (all waves)
-            // before rows 2-3 read its first fragments, and every wave's reads
-            // of stage s are complete, so the next iteration may refill it.
-            mfma_rows<3, 4, 0, 0, CHECK, 0, 2, 2>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
-                                                  ra, rb, kf, kend);
-            __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
-            barrier_no_fence();
-            mfma_rows<3, 4, 0, 0, CHECK, 2, 4, 2>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + nxt,
-                                                  ra, rb, kf, kend);
-            cur = nxt;
-        }
     }
 }
 
@@ -910,7 +868,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 32, SN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-    static_assert((BK == 32 && NS >= 4) || (BK == 64 && NS == 2), "unsupported pipeline shape");
+    static_assert(BK == 32 && NS >= 4, "unsupported pipeline shape");
     using OpA = DmaOperand<A_K, BM, NT, SM, BK>;
     using OpB = DmaOperand<B_K, BN, NT, SN, BK>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
@@ -1043,30 +1001,17 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 // t0g_gemm_<BM>x<BN>_k64_<layout>_<out>[_u]   (_u: element-wise loads for
 // shapes whose rows are not 16-byte aligned)
 // ---------------------------------------------------------------------------
-// 256x256 tiles hold 256 fp32 accumulators per lane: one wave per SIMD, the
-// whole 512-entry VGPR+AGPR file.  Smaller tiles leave room for two workgroups
-// per CU (LDS 64 KB or less each).
-#if T0G_PINGPONG
-#define T0G_WPE_256x256 2, 2
-#else
-#define T0G_WPE_256x256 1, 1
-#endif
+// 128x128 and 64x64 tiles leave room for two or four workgroups per CU (LDS
+// 64 KB or less each); they keep a 4-deep ring of BK 32 stages.  (256x256 is
+// defined further down.)
 #define T0G_WPE_128x128 1, 2
 #define T0G_WPE_64x64 1, 4
-// Fast-path pipeline (K values per stage, stages): 256x256 double-buffers
-// 2 x 64 KB stages of BK 64 (whole 128-byte rows per request, one workgroup per
-// CU); the smaller tiles, which share a CU, keep a 4-deep ring of BK 32 stages.
-#define T0G_PIPE_256x256 64, 2
 #define T0G_PIPE_128x128 32, 4
 #define T0G_PIPE_64x64 32, 4
 #define T0G_GEMM(NAME, BM, BN, WM, WN, AK, BKM, OBF, AL)                                       \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                   \
         __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmArgs p) {          \
-        if constexpr (AL && BM == 256 && T0G_PINGPONG)                                           \
-            t0g::gemm_tile_pp<AK, BKM, OBF>(p);                                                  \
-        else if constexpr (AL && BM == 256 && T0G_MFMA16)                                        \
-            t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                              \
-        else if constexpr (AL)                                                                   \
+        if constexpr (AL)                                                                        \
             t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_##BM##x##BN>(p);            \
         else                                                                                     \
             t0g::gemm_tile<BM, BN, WM, WN, AK, BKM, OBF, AL>(p);                                 \
@@ -1105,11 +1050,24 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, f32, false)     \
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, bf16, true)
 
-#if T0G_PINGPONG
-T0G_GEMM_TILE(t0g_gemm_256x256_k64, 256, 256, 2, 4)
-#else
-T0G_GEMM_TILE(t0g_gemm_256x256_k64, 256, 256, 2, 2)
-#endif
+// 256x256: 8 waves in ping-pong when A is K-contiguous (NN, NT), else the
+// 4-wave kernel (TN, TT: both operands are read with transposing LDS loads,
+// and 8 waves would read half as many fragments again per CU).
+#define T0G_GEMM_256(NAME, AK, BKM, OBF)                                                                  \
+    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
+        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmArgs p) {                \
+        if constexpr (AK)                                                                                 \
+            t0g::gemm_tile_pp<AK, BKM, OBF>(p);                                                          \
+        else                                                                                              \
+            t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                                      \
+    }
+#define T0G_GEMM_LAYOUTS_256(OUTN, OBF)                                 \
+    T0G_GEMM_256(t0g_gemm_256x256_k64_nt_##OUTN, true, true, OBF)       \
+    T0G_GEMM_256(t0g_gemm_256x256_k64_nn_##OUTN, true, false, OBF)      \
+    T0G_GEMM_256(t0g_gemm_256x256_k64_tn_##OUTN, false, false, OBF)     \
+    T0G_GEMM_256(t0g_gemm_256x256_k64_tt_##OUTN, false, true, OBF)
+T0G_GEMM_LAYOUTS_256(f32, false)
+T0G_GEMM_LAYOUTS_256(bf16, true)
 T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)

@@ -172,6 +172,7 @@ struct GemmPlan {
     uint32_t splits;
     uint32_t k_per_split;
     uint32_t tiles_m, tiles_n;
+    uint32_t wg;   // threads per workgroup of the chosen kernel
     std::string symbol;
 };
 
@@ -216,6 +217,11 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, boo
     // measured 10 % faster on 256x256x32768 split 16, while 128x128 gained
     // nothing on 128x4096x4096 split 8 and keeps its 4-stage ring).
     const bool deep = aligned && tile->bm == 64 && (uint64_t)p->tiles_m * p->tiles_n * sk <= kNumCUs;
+    // The 256x256 kernels with a K-contiguous A (NN, NT) run 8 waves in
+    // ping-pong; with an M-contiguous A (TN, TT) every fragment is a transposed
+    // LDS read and the 4-wave kernel, with half the fragment reads per CU, is
+    // faster.
+    p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
                 ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (deep ? "_d" : "") : "_u");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
@@ -290,7 +296,7 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     const uint64_t esize = reduce || !p.out_bf16 ? 4 : 2;
     if ((args.c & 15) == 0 && ((uint64_t)args.ldc * esize) % 16 == 0 && args.c_split_stride % 16 == 0)
         args.flags |= T0G_FLAG_C_VEC;
-    rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.tile->wg, &args, sizeof args);
+    rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.wg, &args, sizeof args);
     if (rc || !reduce) return rc;
 
     hipFunction_t fr = nullptr;
