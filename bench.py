@@ -36,10 +36,12 @@ def make_inputs(torch, m, n, k, layout, seed):
     return a, b
 
 
-def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None):
+def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None, epilogue_ops=None):
     a, b = make_inputs(torch, m, n, k, layout, seed)
     c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16)
+    bias = torch.linspace(-1.0, 1.0, n, device="cuda", dtype=torch.float32)
+    desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16,
+                         epilogue_ops=epilogue_ops, bias=bias.data_ptr() if epilogue_ops else 0)
     kname = t0g.gemm_kernel_name(desc)
     for _ in range(warmup):
         rt.gemm_desc(desc)
@@ -248,6 +250,13 @@ def main():
                            "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1),
                            "frac_of_hbm": round(r["bytes_min"] / sec / 1e9 / PEAK_GBS, 4),
                            "us_per_gemm": round(sec * 1e6, 2), "kernel": r["kernel"]}
+        log("[bench] 4096^3 NN bf16 with fused bias + SiLU epilogue")
+        rf = time_gemm(t0g, torch, rt, stream, M, N, K, "NN", args.steps, args.warmup // 2, epilogue_ops=["bias", "silu"])
+        tf = rf["flop"] / (rf["event_ms_per_launch"] * 1e-3) / 1e12
+        extra["gemm_nn_4096^3_bias_silu"] = {
+            "tflops": round(tf, 2), "ms_per_launch": round(rf["event_ms_per_launch"], 4),
+            "overhead_vs_plain_pct": round((rf["event_ms_per_launch"] / main_res["event_ms_per_launch"] - 1) * 100, 2),
+            "kernel": rf["kernel"]}
         log("[bench] MLP step")
         extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
                                                      max(2, args.warmup // 10))

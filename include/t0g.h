@@ -58,6 +58,23 @@ typedef enum t0g_epilogue {
     T0G_EPI_BIAS_ADD_RELU = 2
 } t0g_epilogue;
 
+/* EpilogueOp of tile_ir (src/t0/tile_ir.rs:41-62): the fused epilogue chain,
+ * applied in order to every fp32 result before the output conversion
+ * (emit_epilogue_on_vreg, src/t0/tile_ir.rs:2213-2339).  A chain is packed into
+ * a uint32_t, 4 bits per op, first op in bits 0-3, 0 ends it (at most 8 ops);
+ * t0g_epilogue_chain builds one.  The gemm_gen epilogues are the chains
+ * {BIAS_ADD} and {BIAS_ADD, RELU}. */
+typedef enum t0g_epilogue_op {
+    T0G_OP_BIAS_ADD = 1,   /* x += bias[col]                 (needs bias: f32[N])   */
+    T0G_OP_SCALE = 2,      /* x *= epi_scale                                        */
+    T0G_OP_RELU = 3,       /* x = max(x, 0)                                         */
+    T0G_OP_SILU = 4,       /* x = x * sigmoid(x)                                    */
+    T0G_OP_GELU = 5,       /* x = x * sigmoid(1.702 x), the reference's approximation */
+    T0G_OP_ABS = 6,        /* x = |x|                                               */
+    T0G_OP_NEG = 7,        /* x = -x                                                */
+    T0G_OP_CLAMP = 8       /* x = min(max(x, clamp_min), clamp_max)                 */
+} t0g_epilogue_op;
+
 typedef enum t0g_dtype { T0G_F32 = 0, T0G_BF16 = 1 } t0g_dtype;
 
 /* GemmConfig (src/t0/gemm_gen.rs:56-84).  Same fields and meaning; the valid
@@ -134,6 +151,23 @@ T0G_API int t0g_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, ui
 T0G_API int t0g_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
                                  uint32_t m, const t0g_gemm_config *cfg, uint8_t out[44]);
 
+/* TileGemm::with_epilogue (src/t0/tile_ir.rs:435-444): pack n_ops (<= 8)
+ * t0g_epilogue_op values into a chain; n_ops = 0 gives the empty chain 0. */
+T0G_API int t0g_epilogue_chain(const uint32_t *ops, uint32_t n_ops, uint32_t *chain);
+/* The epilogue part of TileGemm::name (src/t0/tile_ir.rs:416-430): "" or
+ * "_op_op..." ("_bias_relu", "_silu", ...). */
+T0G_API int t0g_epilogue_chain_name(uint32_t chain, char *buf, size_t len);
+/* tile_ir kernargs with the epilogue arguments lower_gemm declares after M
+ * (src/t0/tile_ir.rs:661-683): [44-byte build_kernargs_m block][bias u64 if
+ * the chain has BIAS_ADD][epi_scale f32 if SCALE][clamp_min f32, clamp_max f32
+ * if CLAMP], packed (bias lands at the unaligned offset 44).  No reference
+ * builder appends these; the layout is the one the generated kernel reads.
+ * *len receives the size (44 .. 64 bytes). */
+T0G_API int t0g_build_kernargs_m_epilogue(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n,
+                                          uint32_t m, const t0g_gemm_config *cfg, uint32_t chain,
+                                          uint64_t bias, float epi_scale, float clamp_min,
+                                          float clamp_max, uint8_t out[64], size_t *len);
+
 /* Backward helpers (src/t0/gemm_gen.rs:482-542), same argument meaning:
  * forward Y[M,N] = X[M,K] * WT[N,K]^T. */
 T0G_API int t0g_auto_select_backward_data(uint32_t m, uint32_t n_orig, uint32_t k_orig,
@@ -182,8 +216,16 @@ T0G_API int t0g_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kern
 /* tile_ir::lower_gemm twin (src/t0/tile_ir.rs:585): 44-byte kernargs with M @40
  * (+ bias u64 @44 with a bias epilogue, src/compile.rs:93-111 ordering). */
 T0G_API int t0g_tile_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out);
+/* lower_gemm of a TileGemm with an epilogue chain (src/t0/tile_ir.rs:585, 661-683):
+ * takes the kernargs of t0g_build_kernargs_m_epilogue for the same chain.
+ * cfg->epilogue must be T0G_EPI_STORE_F32 (the chain replaces it). */
+T0G_API int t0g_tile_kernel_get_epilogue(t0g_device *dev, const t0g_gemm_config *cfg, uint32_t chain,
+                                         t0g_kernel **out);
 /* GpuKernel::load(&device, &elf, &KernelLoadConfig{workgroup_size, lds_size})
- * (src/kfd/mod.rs:2559-2651, 2655): any gfx950 code object, launched raw. */
+ * (src/kfd/mod.rs:2559-2651, 2655): any gfx950 code object, launched raw.  Its
+ * dispatches pass the kernargs block through unchanged: kernargs_len must be the
+ * kernel's argument segment size (for this library's GEMM kernels,
+ * sizeof(T0gGemmArgs) = 104 bytes). */
 T0G_API int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size,
                             const char *symbol, const uint32_t workgroup_size[3],
                             uint32_t lds_size, t0g_kernel **out);
@@ -213,9 +255,12 @@ typedef struct t0g_gemm_desc {
     uint32_t lda, ldb, ldc;         /* elements; 0 = packed */
     uint32_t transpose;             /* t0g_transpose */
     uint32_t out_dtype;             /* t0g_dtype */
-    uint32_t epilogue;              /* t0g_epilogue */
+    uint32_t epilogue;              /* t0g_epilogue (ignored when epi_chain != 0) */
     uint32_t split_k;               /* 0 = from config / auto_select, 1 = none, >1 forced */
     const t0g_gemm_config *config;  /* NULL = t0g_auto_select(m, k, n) */
+    uint32_t epi_chain;             /* t0g_epilogue_chain; 0 = use epilogue */
+    float epi_scale;                /* T0G_OP_SCALE operand */
+    float clamp_min, clamp_max;     /* T0G_OP_CLAMP bounds */
 } t0g_gemm_desc;
 
 /* Enqueue C = op(A) * op(B) (+ epilogue) on the device stream (asynchronous).

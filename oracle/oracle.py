@@ -187,3 +187,45 @@ def parity(c_gpu, c_ref, k):
     maxabs = float(np.max(np.abs(diff))) if diff.size else 0.0
     bound = 1e-2 * np.sqrt(max(k, 1) / 256.0)
     return (relf <= 5e-3 and maxabs <= bound), relf, maxabs, bound
+
+
+# Epilogue chain: tile_ir's EpilogueOp (src/t0/tile_ir.rs:41-62) as applied by
+# emit_epilogue_on_vreg (src/t0/tile_ir.rs:2213-2339), in fp32 and in chain
+# order.  SiLU is the CPU expectation of the reference's own GPU test
+# (src/t0/tile_ir.rs:5113-5117: x * 1/(1 + exp(-x))); GELU is the sigmoid
+# approximation the reference emits (src/t0/tile_ir.rs:2283-2317:
+# x * sigmoid(1.702 x)), not the tanh form its doc comment names.
+EPI_BIAS, EPI_SCALE, EPI_RELU, EPI_SILU, EPI_GELU, EPI_ABS, EPI_NEG, EPI_CLAMP = range(1, 9)
+EPI_NAMES = {"bias": EPI_BIAS, "scale": EPI_SCALE, "relu": EPI_RELU, "silu": EPI_SILU, "gelu": EPI_GELU,
+             "abs": EPI_ABS, "neg": EPI_NEG, "clamp": EPI_CLAMP}
+
+
+def _sigmoid_f32(y):
+    with np.errstate(over="ignore"):
+        return np.float32(1.0) / (np.float32(1.0) + np.exp(-y))
+
+
+def epilogue_chain(c, ops, bias=None, scale=1.0, clamp=(0.0, 0.0)):
+    """Apply a tile_ir epilogue chain (op codes or names) to fp32 results c[M][N]."""
+    x = np.array(c, dtype=np.float32, copy=True)
+    for op in ops:
+        op = EPI_NAMES[op] if isinstance(op, str) else op
+        if op == EPI_BIAS:
+            x = x + np.asarray(bias, dtype=np.float32)[None, :]
+        elif op == EPI_SCALE:
+            x = x * np.float32(scale)
+        elif op == EPI_RELU:
+            x = np.maximum(x, np.float32(0.0))
+        elif op == EPI_SILU:
+            x = x * _sigmoid_f32(x)
+        elif op == EPI_GELU:
+            x = x * _sigmoid_f32(x * np.float32(1.702))
+        elif op == EPI_ABS:
+            x = np.abs(x)
+        elif op == EPI_NEG:
+            x = -x
+        elif op == EPI_CLAMP:
+            x = np.minimum(np.maximum(x, np.float32(clamp[0])), np.float32(clamp[1]))
+        else:
+            raise ValueError(f"unknown epilogue op {op}")
+    return x

@@ -213,8 +213,8 @@ struct TileLoader<false, ROWS, NT, ALIGNED> {
 };
 
 // ---------------------------------------------------------------------------
-// Epilogue: acc -> (+bias[col]) -> (ReLU) -> f32 or bf16 (round to nearest
-// even), masked to the M x N output.  32x32 MFMA result layout: lane
+// Epilogue: acc -> epilogue chain -> f32 or bf16 (round to nearest even),
+// masked to the M x N output.  32x32 MFMA result layout: lane
 // (l32 = lane % 32, g = lane / 32), register r holds row 8*(r/4) + 4*g + r%4,
 // column l32 of the 32x32 block.
 // ---------------------------------------------------------------------------
@@ -225,7 +225,7 @@ template <int SN>
 __device__ __forceinline__ void load_bias_cols(const T0gGemmArgs& p, uint32_t col0, uint32_t l32, float (&bv)[SN]) {
 #pragma unroll
     for (int j = 0; j < SN; ++j) bv[j] = 0.0f;
-    if (p.epilogue != 0) {
+    if (p.flags & T0G_FLAG_BIAS) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
 #pragma unroll
@@ -235,10 +235,75 @@ __device__ __forceinline__ void load_bias_cols(const T0gGemmArgs& p, uint32_t co
     }
 }
 
-__device__ __forceinline__ float apply_epilogue(float x, float bv, uint32_t epi) {
-    if (epi != 0) x = x + bv;
-    if (epi == 2) x = x > 0.0f ? x : 0.0f;
+// The epilogue chain (tile_ir's emit_epilogue_on_vreg, src/t0/tile_ir.rs:2213-2339):
+// T0G_EPI_OP_* codes 4 bits each, first op in the low bits.  The chain is a
+// kernel argument, so the decode loop branches uniformly.  SiLU and GELU use
+// the hardware exp2 and reciprocal, as the reference does: sigmoid(y) =
+// rcp(1 + exp2(-y * log2 e)); GELU is the reference's x * sigmoid(1.702 x).
+struct EpiParams {
+    uint32_t chain;
+    float scale, lo, hi;
+};
+
+__device__ __forceinline__ float epi_sigmoid_mul(float x, float y) {
+    const float e = __builtin_amdgcn_exp2f(-y * 1.44269504f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float apply_epilogue(float x, float bv, const EpiParams& e) {
+    for (uint32_t c = e.chain; c != 0; c >>= 4) {
+        switch (c & 15u) {
+        case T0G_EPI_OP_BIAS_ADD: x = x + bv; break;
+        case T0G_EPI_OP_SCALE: x = x * e.scale; break;
+        case T0G_EPI_OP_RELU: x = x > 0.0f ? x : 0.0f; break;
+        case T0G_EPI_OP_SILU: x = epi_sigmoid_mul(x, x); break;
+        case T0G_EPI_OP_GELU: x = epi_sigmoid_mul(x, x * 1.702f); break;
+        case T0G_EPI_OP_ABS: x = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & 0x7FFFFFFFu); break;
+        case T0G_EPI_OP_NEG: x = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) ^ 0x80000000u); break;
+        case T0G_EPI_OP_CLAMP: x = __builtin_fminf(__builtin_fmaxf(x, e.lo), e.hi); break;
+        default: break;
+        }
+    }
     return x;
+}
+
+template <class Args>
+__device__ __forceinline__ EpiParams epi_of(const Args& p) {
+    return EpiParams{p.epilogue, p.epi_scale, p.clamp_lo, p.clamp_hi};
+}
+
+// The chain over a lane's N output values: one decode per op rather than per
+// value, which keeps the unrolled store loops small.
+template <int N>
+__device__ __forceinline__ void apply_epilogue_n(float (&v)[N], const float (&bv)[N], const EpiParams& e) {
+    for (uint32_t c = e.chain; c != 0; c >>= 4) {
+        const uint32_t op = c & 15u;
+        if (op == T0G_EPI_OP_BIAS_ADD) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = v[i] + bv[i];
+        } else if (op == T0G_EPI_OP_SCALE) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = v[i] * e.scale;
+        } else if (op == T0G_EPI_OP_RELU) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
+        } else if (op == T0G_EPI_OP_SILU) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = epi_sigmoid_mul(v[i], v[i]);
+        } else if (op == T0G_EPI_OP_GELU) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = epi_sigmoid_mul(v[i], v[i] * 1.702f);
+        } else if (op == T0G_EPI_OP_ABS) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[i]) & 0x7FFFFFFFu);
+        } else if (op == T0G_EPI_OP_NEG) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[i]) ^ 0x80000000u);
+        } else if (op == T0G_EPI_OP_CLAMP) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] = __builtin_fminf(__builtin_fmaxf(v[i], e.lo), e.hi);
+        }
+    }
 }
 
 template <int SM, int SN, bool OUT_BF16>
@@ -257,7 +322,7 @@ __device__ __forceinline__ void store_tile(const T0gGemmArgs& p, const f32x16_t 
             for (int r = 0; r < 16; ++r) {
                 const uint32_t row = row0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (col_ok && row < p.m) {
-                    const float x = apply_epilogue(acc[i][j][r], bv[j], p.epilogue);
+                    const float x = apply_epilogue(acc[i][j][r], bv[j], epi_of(p));
                     const uint64_t idx = (uint64_t)row * p.ldc + col;
                     if constexpr (OUT_BF16)
                         reinterpret_cast<gbf16_t*>(cbase)[idx] = (__bf16)x;
@@ -298,7 +363,7 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
     float bv[kCols];
 #pragma unroll
     for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
-    if (p.epilogue != 0) {
+    if (p.flags & T0G_FLAG_BIAS) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
 #pragma unroll
@@ -330,8 +395,7 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
                 v[c + 2] = q[2];
                 v[c + 3] = q[3];
             }
-#pragma unroll
-            for (int c = 0; c < kCols; ++c) v[c] = apply_epilogue(v[c], bv[c], p.epilogue);
+            apply_epilogue_n<kCols>(v, bv, epi_of(p));
             const uint32_t grow = row0 + i * 32 + rr, gcol = col0 + cl;
             const uint64_t addr = cbase + ((uint64_t)grow * p.ldc + gcol) * esize;
             if (vec) {
@@ -962,7 +1026,8 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
             }
             float x[4] = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) x[c] = apply_epilogue(x[c], p.epilogue != 0 ? bias[col + c] : 0.0f, p.epilogue);
+            for (int c = 0; c < 4; ++c)
+                x[c] = apply_epilogue(x[c], (p.flags & T0G_REDUCE_BIAS) ? bias[col + c] : 0.0f, epi_of(p));
             const uint64_t o = (uint64_t)row * p.ldc + col;
             if constexpr (OUT_BF16) {
                 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -985,7 +1050,7 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
         const size_t w = (size_t)row * p.ldw + col;
         float acc = 0.0f;
         for (uint32_t s = 0; s < p.splits; ++s) acc = acc + ws[s * p.plane_elems + w];
-        acc = apply_epilogue(acc, p.epilogue != 0 ? bias[col] : 0.0f, p.epilogue);
+        acc = apply_epilogue(acc, (p.flags & T0G_REDUCE_BIAS) ? bias[col] : 0.0f, epi_of(p));
         const size_t o = (size_t)row * p.ldc + col;
         if constexpr (OUT_BF16)
             reinterpret_cast<gbf16_t*>((uintptr_t)p.c)[o] = (__bf16)acc;

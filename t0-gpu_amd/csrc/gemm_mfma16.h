@@ -184,8 +184,16 @@ __device__ __forceinline__ void mfma16(f32x4_t& acc, const bf16x8_t& a, const bf
 
 // Wait states between the last MFMA writing an accumulator and VALU reads of
 // it (8-pass XDL result to VALU read: at most 19), and between VALU writes of
-// accumulators and their first use as MFMA source C.
-__device__ __forceinline__ void mfma16_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+// accumulators and their first use as MFMA source C.  The scheduling barrier
+// keeps the compiler from moving accumulator reads or writes across it.  The
+// accumulators must also never live in scratch: a spill store right after an
+// asm MFMA would read its result too early (the Makefile rejects a build in
+// which these kernels use scratch).
+__device__ __forceinline__ void mfma16_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // One 32-wide K step, rows [RB, RE) of SM sub-tile rows, SN MFMAs per row.
 // Next-step fragment reads go to rows [RR, RE): with all rows, A[r] in row r
@@ -334,7 +342,7 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
     float bv[kCols];
 #pragma unroll
     for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
-    if (p.epilogue != 0) {
+    if (p.flags & T0G_FLAG_BIAS) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
 #pragma unroll
@@ -369,8 +377,7 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
                 v[c + 2] = qv[2];
                 v[c + 3] = qv[3];
             }
-#pragma unroll
-            for (int c = 0; c < kCols; ++c) v[c] = apply_epilogue(v[c], bv[c], p.epilogue);
+            apply_epilogue_n<kCols>(v, bv, epi_of(p));
             const uint32_t grow = row0 + i2 * 16 + rr, gcol = col0 + cl;
             const uint64_t addr = cbase + ((uint64_t)grow * p.ldc + gcol) * esize;
             if (vec) {

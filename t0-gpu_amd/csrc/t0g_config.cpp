@@ -132,6 +132,38 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
     make_config(*best, best_sk, out);
 }
 
+uint32_t legacy_chain(uint32_t epilogue) {
+    if (epilogue == T0G_EPI_BIAS_ADD) return T0G_OP_BIAS_ADD;
+    if (epilogue == T0G_EPI_BIAS_ADD_RELU) return T0G_OP_BIAS_ADD | (T0G_OP_RELU << 4);
+    return 0;
+}
+
+int check_chain(uint32_t chain) {
+    bool ended = false;
+    for (uint32_t i = 0; i < kMaxChainOps; ++i) {
+        const uint32_t op = (chain >> (4 * i)) & 15u;
+        if (op == 0) {
+            ended = true;
+        } else if (ended || op > T0G_OP_CLAMP) {
+            return fail(T0G_ERR_INVALID_ARG, "bad epilogue chain 0x%08x (op %u at position %u)", chain, op, i);
+        }
+    }
+    return T0G_OK;
+}
+
+bool chain_has(uint32_t chain, uint32_t op) {
+    for (uint32_t c = chain; c != 0; c >>= 4)
+        if ((c & 15u) == op) return true;
+    return false;
+}
+
+// lower_gemm declares bias, epi_scale, clamp_min, clamp_max after M, each only
+// if some op of the chain uses it (src/t0/tile_ir.rs:670-683).
+uint32_t chain_kernarg_bytes(uint32_t chain) {
+    return (chain_has(chain, T0G_OP_BIAS_ADD) ? 8u : 0u) + (chain_has(chain, T0G_OP_SCALE) ? 4u : 0u) +
+           (chain_has(chain, T0G_OP_CLAMP) ? 8u : 0u);
+}
+
 }  // namespace t0g
 
 using namespace t0g;
@@ -280,6 +312,56 @@ int t0g_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32
     put_u32(out + 32, shift);
     put_u32(out + 36, 0);
     put_u32(out + 40, m);
+    return ok();
+}
+
+int t0g_epilogue_chain(const uint32_t *ops, uint32_t n_ops, uint32_t *chain) {
+    if (!chain || (n_ops && !ops)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (n_ops > kMaxChainOps) return fail(T0G_ERR_INVALID_ARG, "%u epilogue ops, at most %u", n_ops, kMaxChainOps);
+    uint32_t c = 0;
+    for (uint32_t i = 0; i < n_ops; ++i) {
+        if (ops[i] < T0G_OP_BIAS_ADD || ops[i] > T0G_OP_CLAMP)
+            return fail(T0G_ERR_INVALID_ARG, "bad epilogue op %u", ops[i]);
+        c |= ops[i] << (4 * i);
+    }
+    *chain = c;
+    return ok();
+}
+
+int t0g_epilogue_chain_name(uint32_t chain, char *buf, size_t len) {
+    if (!buf || !len) return fail(T0G_ERR_INVALID_ARG, "NULL buffer");
+    int rc = check_chain(chain);
+    if (rc) return rc;
+    static const char *const kNames[] = {"", "bias", "scale", "relu", "silu", "gelu", "abs", "neg", "clamp"};
+    std::string s;
+    for (uint32_t c = chain; c != 0; c >>= 4) s += std::string("_") + kNames[c & 15u];
+    if (s.size() + 1 > len) return fail(T0G_ERR_INVALID_ARG, "name buffer too small");
+    memcpy(buf, s.c_str(), s.size() + 1);
+    return ok();
+}
+
+int t0g_build_kernargs_m_epilogue(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
+                                  const t0g_gemm_config *cfg, uint32_t chain, uint64_t bias, float epi_scale,
+                                  float clamp_min, float clamp_max, uint8_t out[64], size_t *len) {
+    if (!out || !len) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    int rc = check_chain(chain);
+    if (rc) return rc;
+    if ((rc = t0g_build_kernargs_m(x, wt, y, k, n, m, cfg, out))) return rc;
+    size_t off = 44;
+    if (chain_has(chain, T0G_OP_BIAS_ADD)) {
+        put_u64(out + off, bias);
+        off += 8;
+    }
+    if (chain_has(chain, T0G_OP_SCALE)) {
+        memcpy(out + off, &epi_scale, 4);
+        off += 4;
+    }
+    if (chain_has(chain, T0G_OP_CLAMP)) {
+        memcpy(out + off, &clamp_min, 4);
+        memcpy(out + off + 4, &clamp_max, 4);
+        off += 8;
+    }
+    *len = off;
     return ok();
 }
 

@@ -41,6 +41,13 @@ int validate(const t0g_gemm_config *cfg);
 void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
 double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);
 
+// Epilogue chains (t0g_epilogue_op codes, 4 bits each, first op lowest).
+constexpr uint32_t kMaxChainOps = 8;
+uint32_t legacy_chain(uint32_t epilogue);          // t0g_epilogue -> chain
+int check_chain(uint32_t chain);                   // codes valid, no gaps
+bool chain_has(uint32_t chain, uint32_t op);
+uint32_t chain_kernarg_bytes(uint32_t chain);      // tile_ir arguments after M
+
 }  // namespace t0g
 
 #endif

@@ -18,9 +18,14 @@ typedef struct T0gGemmArgs {
     uint32_t k_per_split;    /* K elements per split slice (multiple of tile_k)   */
     uint32_t tiles_m;        /* output tiles along M covered by the grid          */
     uint32_t tiles_n;        /* output tiles along N covered by the grid          */
-    uint32_t epilogue;       /* 0 store, 1 +bias[col], 2 +bias[col] then ReLU     */
+    uint32_t epilogue;       /* epilogue chain, T0G_EPI_OP_* codes 4 bits each, first
+                                op in bits 0-3, 0 ends the chain (0: plain store)   */
     uint32_t group_m;        /* tile-order group height (L2 reuse), >= 1          */
     uint32_t flags;          /* T0G_FLAG_* bits                                   */
+    float epi_scale;         /* Scale operand                                     */
+    float clamp_lo;          /* Clamp bounds                                      */
+    float clamp_hi;
+    uint32_t reserved;
 } T0gGemmArgs;
 
 typedef struct T0gReduceArgs {
@@ -30,13 +35,30 @@ typedef struct T0gReduceArgs {
     uint64_t plane_elems;    /* elements between planes                           */
     uint32_t m, n, ldw, ldc;
     uint32_t splits;
-    uint32_t epilogue;
+    uint32_t epilogue;       /* epilogue chain, as in T0gGemmArgs                 */
     uint32_t grid_blocks;    /* launched workgroups (256 threads each)           */
-    uint32_t flags;          /* T0G_REDUCE_VEC                                    */
+    uint32_t flags;          /* T0G_REDUCE_* bits                                 */
+    float epi_scale;
+    float clamp_lo;
+    float clamp_hi;
+    uint32_t reserved;
 } T0gReduceArgs;
 
 #define T0G_FLAG_XCD_REMAP 1u   /* remap block ids so each XCD owns a contiguous tile range */
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
+#define T0G_FLAG_BIAS 4u        /* the chain reads bias[col]                                     */
 #define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
+#define T0G_REDUCE_BIAS 2u      /* the chain reads bias[col]                                     */
+
+/* Epilogue chain operations: tile_ir's EpilogueOp (src/t0/tile_ir.rs:41-62),
+ * applied in chain order to each fp32 result before the output conversion. */
+#define T0G_EPI_OP_BIAS_ADD 1u  /* x += bias[col]                                  */
+#define T0G_EPI_OP_SCALE 2u     /* x *= epi_scale                                  */
+#define T0G_EPI_OP_RELU 3u      /* x = max(x, 0)                                   */
+#define T0G_EPI_OP_SILU 4u      /* x = x * sigmoid(x)                              */
+#define T0G_EPI_OP_GELU 5u      /* x = x * sigmoid(1.702 x)                        */
+#define T0G_EPI_OP_ABS 6u       /* x = |x|                                         */
+#define T0G_EPI_OP_NEG 7u       /* x = -x                                          */
+#define T0G_EPI_OP_CLAMP 8u     /* x = min(max(x, clamp_lo), clamp_hi)             */
 
 #endif

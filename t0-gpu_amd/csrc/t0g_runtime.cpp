@@ -51,6 +51,7 @@ struct t0g_kernel {
     uint32_t wg[3] = {1, 1, 1};
     uint32_t lds = 0;
     uint32_t kernarg_size = 0;
+    uint32_t chain = 0;           // TileGemm: epilogue chain its kernargs carry
     std::string name;
 };
 
@@ -256,7 +257,8 @@ static int ensure_workspace(t0g_device *dev, size_t bytes) {
 struct GemmOperands {
     uint64_t a, b, c, bias;
     uint32_t m, n, k, lda, ldb, ldc;
-    uint32_t epilogue;
+    uint32_t chain;            // epilogue chain (t0g_epilogue_op codes)
+    float epi_scale, clamp_lo, clamp_hi;
     uint64_t c_split_stride;   // reference-layout path: caller-owned planes
 };
 
@@ -285,13 +287,17 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
         args.c = ws;
         args.ldc = o.n;
         args.c_split_stride = (uint64_t)o.m * o.n * 4;
-        args.epilogue = T0G_EPI_STORE_F32;
+        args.epilogue = 0;
     } else {
         args.c = o.c;
         args.ldc = o.ldc;
         args.c_split_stride = o.c_split_stride;
-        args.epilogue = o.epilogue;
+        args.epilogue = o.chain;
+        args.epi_scale = o.epi_scale;
+        args.clamp_lo = o.clamp_lo;
+        args.clamp_hi = o.clamp_hi;
         args.bias = o.bias;
+        if (chain_has(o.chain, T0G_OP_BIAS_ADD)) args.flags |= T0G_FLAG_BIAS;
     }
     const uint64_t esize = reduce || !p.out_bf16 ? 4 : 2;
     if ((args.c & 15) == 0 && ((uint64_t)args.ldc * esize) % 16 == 0 && args.c_split_stride % 16 == 0)
@@ -313,7 +319,11 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     r.ldw = o.n;
     r.ldc = o.ldc;
     r.splits = p.splits;
-    r.epilogue = o.epilogue;
+    r.epilogue = o.chain;
+    r.epi_scale = o.epi_scale;
+    r.clamp_lo = o.clamp_lo;
+    r.clamp_hi = o.clamp_hi;
+    if (chain_has(o.chain, T0G_OP_BIAS_ADD)) r.flags |= T0G_REDUCE_BIAS;
     const uint64_t out_esize = p.out_bf16 ? 2 : 4;
     const bool vec = (ws & 15) == 0 && (o.n & 3) == 0 && (o.c & (4 * out_esize - 1)) == 0 &&
                      ((uint64_t)o.ldc * out_esize) % (4 * out_esize) == 0 && (uint64_t)o.m * (o.n / 4) < (1ull << 31);
@@ -330,7 +340,9 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
     if (d->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", d->transpose);
     if (d->out_dtype > T0G_BF16) return fail(T0G_ERR_INVALID_ARG, "bad out_dtype %u", d->out_dtype);
     if (d->epilogue > T0G_EPI_BIAS_ADD_RELU) return fail(T0G_ERR_INVALID_ARG, "bad epilogue %u", d->epilogue);
-    if (d->epilogue != T0G_EPI_STORE_F32 && !d->bias)
+    const uint32_t chain = d->epi_chain ? d->epi_chain : legacy_chain(d->epilogue);
+    if (int rc0 = check_chain(chain)) return rc0;
+    if (chain_has(chain, T0G_OP_BIAS_ADD) && !d->bias)
         return fail(T0G_ERR_INVALID_ARG, "bias epilogue without a bias pointer");
     const uint32_t t = d->transpose;
     o->a = d->a;
@@ -343,7 +355,10 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
     o->lda = d->lda ? d->lda : (a_k_major(t) ? d->k : d->m);
     o->ldb = d->ldb ? d->ldb : (b_k_major(t) ? d->k : d->n);
     o->ldc = d->ldc ? d->ldc : d->n;
-    o->epilogue = d->epilogue;
+    o->chain = chain;
+    o->epi_scale = d->epi_scale;
+    o->clamp_lo = d->clamp_min;
+    o->clamp_hi = d->clamp_max;
     o->c_split_stride = 0;
     if (o->ldc < o->n) return fail(T0G_ERR_INVALID_ARG, "ldc=%u < n=%u", o->ldc, o->n);
     if (a_k_major(t) ? o->lda < o->k : o->lda < o->m) return fail(T0G_ERR_INVALID_ARG, "lda=%u too small", o->lda);
@@ -355,7 +370,7 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
         select_config(d->m ? d->m : 1, d->k, d->n ? d->n : 1, cfg);
     }
     cfg->transpose = t;
-    cfg->epilogue = d->epilogue;
+    cfg->epilogue = d->epi_chain ? (uint32_t)T0G_EPI_STORE_F32 : d->epilogue;
     if ((rc = validate(cfg))) return rc;
     if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
     if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
@@ -525,15 +540,23 @@ int t0g_memset(t0g_device *dev, uint64_t dst, int value, size_t bytes) {
     return ok();
 }
 
-static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, KernelKind kind, t0g_kernel **out) {
+// chain != 0 (TileGemm only): an explicit epilogue chain; its arguments follow
+// M in the kernargs.  Otherwise the chain is cfg->epilogue's.
+static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, KernelKind kind, uint32_t chain,
+                             t0g_kernel **out) {
     if (!dev || !cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
     *out = nullptr;
     int rc = validate(cfg);
     if (rc) return rc;
+    if ((rc = check_chain(chain))) return rc;
+    if (chain && cfg->epilogue != T0G_EPI_STORE_F32)
+        return fail(T0G_ERR_INVALID_ARG, "an epilogue chain replaces cfg->epilogue, which must be STORE_F32");
     if (cfg->transpose != T0G_NT && cfg->transpose != T0G_NN)
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "reference-layout kernels are NT or NN");
-    char name[128];
+    char name[160], epi[64];
     t0g_config_name(cfg, name, sizeof name);
+    t0g_epilogue_chain_name(chain, epi, sizeof epi);
+    strncat(name, epi, sizeof name - strlen(name) - 1);
     std::string key = std::string(kind == KernelKind::TileGemm ? "tile:" : "gen:") + name;
     std::lock_guard<std::mutex> lk(dev->mu);
     auto it = dev->kernel_cache.find(key);
@@ -546,10 +569,11 @@ static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, Kernel
     k->cfg = *cfg;
     k->wg[0] = cfg->wg_size;
     k->lds = t0g_config_lds_total(cfg);
+    k->chain = chain ? chain : legacy_chain(cfg->epilogue);
     if (kind == KernelKind::GemmGen)
         k->kernarg_size = cfg->epilogue != T0G_EPI_STORE_F32 ? 48 : 40;
     else
-        k->kernarg_size = cfg->epilogue != T0G_EPI_STORE_F32 ? 52 : 44;
+        k->kernarg_size = 44 + chain_kernarg_bytes(k->chain);
     k->name = name;
     *out = k.get();
     dev->kernel_cache.emplace(key, k.get());
@@ -558,11 +582,15 @@ static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, Kernel
 }
 
 int t0g_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out) {
-    return kernel_get_common(dev, cfg, KernelKind::GemmGen, out);
+    return kernel_get_common(dev, cfg, KernelKind::GemmGen, 0, out);
 }
 
 int t0g_tile_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g_kernel **out) {
-    return kernel_get_common(dev, cfg, KernelKind::TileGemm, out);
+    return kernel_get_common(dev, cfg, KernelKind::TileGemm, 0, out);
+}
+
+int t0g_tile_kernel_get_epilogue(t0g_device *dev, const t0g_gemm_config *cfg, uint32_t chain, t0g_kernel **out) {
+    return kernel_get_common(dev, cfg, KernelKind::TileGemm, chain, out);
 }
 
 int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size, const char *symbol,
@@ -644,13 +672,27 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
     o.n = rd_u32(ka + 28);
     const uint32_t y_split_stride = rd_u32(ka + 36);
     if (kn->kind == KernelKind::TileGemm) {
+        // lower_gemm's argument order after M: bias, epi_scale, clamp_min, clamp_max
+        // (src/t0/tile_ir.rs:661-683), each present only if the chain uses it.
         o.m = rd_u32(ka + 40);
-        if (cfg.epilogue != T0G_EPI_STORE_F32) o.bias = rd_u64(ka + 44);
+        size_t off = 44;
+        if (chain_has(kn->chain, T0G_OP_BIAS_ADD)) {
+            o.bias = rd_u64(ka + off);
+            off += 8;
+        }
+        if (chain_has(kn->chain, T0G_OP_SCALE)) {
+            memcpy(&o.epi_scale, ka + off, 4);
+            off += 4;
+        }
+        if (chain_has(kn->chain, T0G_OP_CLAMP)) {
+            memcpy(&o.clamp_lo, ka + off, 4);
+            memcpy(&o.clamp_hi, ka + off + 4, 4);
+        }
     } else if (cfg.epilogue != T0G_EPI_STORE_F32) {
         o.bias = rd_u64(ka + 40);
     }
     if (o.m == 0) o.m = tiles_m * cfg.tile_m;   // gemm_gen kernargs carry no M: the grid covers it exactly
-    o.epilogue = cfg.epilogue;
+    o.chain = kn->chain;
     o.lda = o.k;
     o.ldb = cfg.transpose == T0G_NN ? o.n : o.k;
     o.ldc = o.n;

@@ -40,6 +40,10 @@ NT, NN, TN, TT = 0, 1, 2, 3
 LAYOUTS = {"NT": NT, "NN": NN, "TN": TN, "TT": TT}
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
 F32, BF16 = 0, 1
+# tile_ir EpilogueOp (src/t0/tile_ir.rs:41-62): the fused epilogue chain
+OP_BIAS_ADD, OP_SCALE, OP_RELU, OP_SILU, OP_GELU, OP_ABS, OP_NEG, OP_CLAMP = range(1, 9)
+EPILOGUE_OPS = {"bias": OP_BIAS_ADD, "scale": OP_SCALE, "relu": OP_RELU, "silu": OP_SILU,
+                "gelu": OP_GELU, "abs": OP_ABS, "neg": OP_NEG, "clamp": OP_CLAMP}
 
 
 class T0gError(RuntimeError):
@@ -122,6 +126,10 @@ class GemmDesc(ctypes.Structure):
         ("epilogue", ctypes.c_uint32),
         ("split_k", ctypes.c_uint32),
         ("config", ctypes.POINTER(GemmConfig)),
+        ("epi_chain", ctypes.c_uint32),
+        ("epi_scale", ctypes.c_float),
+        ("clamp_min", ctypes.c_float),
+        ("clamp_max", ctypes.c_float),
     ]
 
 
@@ -156,6 +164,10 @@ _sig("t0g_build_kernargs", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cf
 _sig("t0g_build_kernargs_with_bias", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, _u64,
      ctypes.c_char_p)
 _sig("t0g_build_kernargs_m", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, ctypes.c_char_p)
+_sig("t0g_epilogue_chain", ctypes.c_int, _u32p, _u32, _u32p)
+_sig("t0g_epilogue_chain_name", ctypes.c_int, _u32, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_build_kernargs_m_epilogue", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp, _u32, _u64,
+     ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_char_p, ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_auto_select_backward_data", ctypes.c_int, _u32, _u32, _u32, _cfgp)
 _sig("t0g_auto_select_backward_weight", ctypes.c_int, _u32, _u32, _u32, _cfgp)
 _sig("t0g_build_kernargs_backward_data", ctypes.c_int, _u64, _u64, _u64, _u32, _u32, _u32, _cfgp,
@@ -178,6 +190,7 @@ _sig("t0g_memcpy_d2h", ctypes.c_int, _p, _p, _u64, ctypes.c_size_t)
 _sig("t0g_memset", ctypes.c_int, _p, _u64, ctypes.c_int, ctypes.c_size_t)
 _sig("t0g_kernel_get", ctypes.c_int, _p, _cfgp, ctypes.POINTER(_p))
 _sig("t0g_tile_kernel_get", ctypes.c_int, _p, _cfgp, ctypes.POINTER(_p))
+_sig("t0g_tile_kernel_get_epilogue", ctypes.c_int, _p, _cfgp, _u32, ctypes.POINTER(_p))
 _sig("t0g_kernel_load", ctypes.c_int, _p, _p, ctypes.c_size_t, ctypes.c_char_p, _u32p, _u32,
      ctypes.POINTER(_p))
 _sig("t0g_kernel_info", ctypes.c_int, _p, _u32p, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t)
@@ -265,6 +278,15 @@ def build_kernargs_m(x, wt, y, k, n, m, cfg):
     return buf.raw
 
 
+def build_kernargs_m_epilogue(x, wt, y, k, n, m, cfg, chain, bias=0, epi_scale=1.0, clamp=(0.0, 0.0)):
+    """build_kernargs_m + the epilogue arguments lower_gemm declares after M (src/t0/tile_ir.rs:661-683)."""
+    buf = ctypes.create_string_buffer(64)
+    ln = ctypes.c_size_t()
+    _check(_lib.t0g_build_kernargs_m_epilogue(x, wt, y, k, n, m, ctypes.byref(cfg), chain, bias, epi_scale,
+                                              clamp[0], clamp[1], buf, ctypes.byref(ln)))
+    return buf.raw[:ln.value]
+
+
 def auto_select_backward_data(m, n_orig, k_orig):
     cfg = GemmConfig()
     _check(_lib.t0g_auto_select_backward_data(m, n_orig, k_orig, ctypes.byref(cfg)))
@@ -297,8 +319,25 @@ def compute_grid_backward_weight(cfg, n_orig, k_orig):
     return _grid2(_lib.t0g_compute_grid_backward_weight, ctypes.byref(cfg), n_orig, k_orig)
 
 
+def epilogue_chain(ops):
+    """TileGemm::with_epilogue (src/t0/tile_ir.rs:440): op codes or names -> packed chain."""
+    codes = [EPILOGUE_OPS[o] if isinstance(o, str) else int(o) for o in ops]
+    arr = (ctypes.c_uint32 * max(1, len(codes)))(*codes)
+    out = ctypes.c_uint32()
+    _check(_lib.t0g_epilogue_chain(arr, len(codes), ctypes.byref(out)))
+    return out.value
+
+
+def epilogue_chain_name(chain):
+    buf = ctypes.create_string_buffer(96)
+    _check(_lib.t0g_epilogue_chain_name(chain, buf, len(buf)))
+    return buf.value.decode()
+
+
 def gemm_desc(a, b, c, m, n, k, transpose=NT, out_dtype=F32, lda=0, ldb=0, ldc=0, split_k=0,
-              epilogue=EPI_STORE_F32, bias=0, workspace=0, workspace_bytes=0, config=None):
+              epilogue=EPI_STORE_F32, bias=0, workspace=0, workspace_bytes=0, config=None,
+              epilogue_ops=None, epi_scale=1.0, clamp=(0.0, 0.0)):
+    """epilogue_ops: a tile_ir epilogue chain (op codes or names); overrides `epilogue`."""
     d = GemmDesc()
     d.a, d.b, d.c, d.bias = a, b, c, bias
     d.workspace, d.workspace_bytes = workspace, workspace_bytes
@@ -309,6 +348,9 @@ def gemm_desc(a, b, c, m, n, k, transpose=NT, out_dtype=F32, lda=0, ldb=0, ldc=0
     d.epilogue = epilogue
     d.split_k = split_k
     d.config = ctypes.pointer(config) if config is not None else None
+    d.epi_chain = epilogue_chain(epilogue_ops) if epilogue_ops else 0
+    d.epi_scale = epi_scale
+    d.clamp_min, d.clamp_max = clamp
     return d
 
 
@@ -431,9 +473,14 @@ class GpuRuntime:
         _check(_lib.t0g_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
         return Kernel(h)
 
-    def ensure_tile_kernel(self, cfg):
+    def ensure_tile_kernel(self, cfg, epilogue_chain=0):
+        """lower_gemm(&spec) + load; epilogue_chain: the spec's tile_ir epilogue (packed)."""
         h = ctypes.c_void_p()
-        _check(_lib.t0g_tile_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        if epilogue_chain:
+            _check(_lib.t0g_tile_kernel_get_epilogue(self.handle, ctypes.byref(cfg), epilogue_chain,
+                                                     ctypes.byref(h)))
+        else:
+            _check(_lib.t0g_tile_kernel_get(self.handle, ctypes.byref(cfg), ctypes.byref(h)))
         return Kernel(h)
 
     def load_kernel(self, code_object, symbol, workgroup_size, lds_size=0):

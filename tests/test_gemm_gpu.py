@@ -466,8 +466,12 @@ def test_raw_kernel_load_and_dispatch(rt, bufs):
     aa, ba = bufs.up(a), bufs.up(b)
     c = bufs.alloc(m * n * 4, fill=0)
     tm, tn = m // 128, n // 128
-    # T0gGemmArgs: a b c bias c_split_stride | m n k lda ldb ldc k_per_split tiles_m tiles_n epilogue group_m flags
-    ka = struct.pack("<QQQQQ" + "I" * 12, aa, ba, c, 0, 0, m, n, k, k, k, n, k, tm, tn, 0, 8, 1)
+    # T0gGemmArgs (t0-gpu_amd/csrc/t0g_kernel_args.h), all 104 bytes: a b c bias c_split_stride |
+    # m n k lda ldb ldc k_per_split tiles_m tiles_n epilogue group_m flags | epi_scale clamp_lo clamp_hi reserved.
+    # The block must be exactly the kernel's argument size.
+    ka = struct.pack("<QQQQQ" + "I" * 12 + "fffI", aa, ba, c, 0, 0, m, n, k, k, k, n, k, tm, tn, 0, 8, 1,
+                     1.0, 0.0, 0.0, 0)
+    assert len(ka) == 104
     rt.dispatch(kern, [tm * tn * 256, 1, 1], ka)
     check_parity(rt.read(c, (m, n), np.float32), o.gemm("NT", a, b, m, n, k), k, "raw dispatch")
 
@@ -508,3 +512,105 @@ def test_injected_failure_poisons_the_device():
     finally:
         t0g.debug_fail_hip_call(0)
         r.close()
+
+
+# ---- fused epilogue chains (tile_ir EpilogueOp, src/t0/tile_ir.rs:41-62) ----
+CHAINS = [("relu",), ("silu",), ("gelu",), ("abs",), ("neg",), ("scale",), ("clamp",), ("bias", "relu"),
+          ("bias", "scale", "silu"), ("gelu", "neg", "abs", "clamp")]
+CHAIN_CASES = [("tile_256x256_k64", "NN"), ("tile_256x256_k64", "TN"), ("tile_128x128_k64", "NT"),
+               ("tile_64x64_k64", "TT")]
+
+
+def _chain_case(m, n, k, layout, seed):
+    a = o.rand_bf16_xorshift(m * k, seed).reshape(m, k)
+    b = o.rand_bf16_xorshift(n * k, seed + 1).reshape(n, k)
+    bias = ((np.arange(n, dtype=np.float32) % 7) - 3.0) * 0.5
+    a_st, b_st = stored_operands(layout, a, b)
+    return a, b, a_st, b_st, bias
+
+
+@pytest.mark.parametrize("chain", CHAINS, ids=["_".join(c) for c in CHAINS])
+@pytest.mark.parametrize("preset,layout", CHAIN_CASES)
+@pytest.mark.parametrize("m,n,k", [(512, 512, 256), (300, 264, 192)])
+def test_epilogue_chains(rt, bufs, chain, preset, layout, m, n, k):
+    """Every op of the chain in the store path of each kernel family (fast paths,
+    edge tiles, the element-wise path), f32 against the oracle and bf16 bit-exact
+    against RNE of the same kernel's f32 result."""
+    a, b, a_st, b_st, bias = _chain_case(m, n, k, layout, 11)
+    kw = dict(epilogue_ops=list(chain), epi_scale=-0.75, clamp=(-0.5, 1.25), bias=bufs.up(bias),
+              config=t0g.GemmConfig.preset(preset), split_k=1)
+    ref = o.epilogue_chain(o.gemm("NT", a, b, m, n, k), chain, bias=bias, scale=-0.75, clamp=(-0.5, 1.25))
+    c32 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, **kw)
+    check_parity(c32, ref, k, f"{'_'.join(chain)} {preset} {layout} {m}x{n}x{k}")
+    c16 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, out=t0g.BF16, **kw)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c32)), "bf16 output is not RNE of the f32 output"
+
+
+@pytest.mark.parametrize("split_k", [4, 16])
+def test_epilogue_chain_after_split_k_reduce(rt, bufs, split_k):
+    """With split-K the chain runs once, in the plane-ordered reduce."""
+    m, n, k = 256, 320, 4096
+    chain = ("bias", "gelu", "scale", "clamp")
+    a, b, a_st, b_st, bias = _chain_case(m, n, k, "NT", 21)
+    ref = o.epilogue_chain(o.gemm("NT", a, b, m, n, k), chain, bias=bias, scale=2.0, clamp=(-1.0, 3.0))
+    kw = dict(epilogue_ops=list(chain), epi_scale=2.0, clamp=(-1.0, 3.0), bias=bufs.up(bias), split_k=split_k)
+    c32 = run_gemm(rt, bufs, "NT", a_st, b_st, m, n, k, **kw)
+    check_parity(c32, ref, k, f"chain after split {split_k}")
+    c16 = run_gemm(rt, bufs, "NT", a_st, b_st, m, n, k, out=t0g.BF16, **kw)
+    assert np.array_equal(c16, o.f32_to_bf16_rne(c32))
+
+
+def _reference_epilogue_inputs(m, k, n):
+    """Inputs of the reference's epilogue GPU tests (src/t0/tile_ir.rs:5036-5039)."""
+    x = ((np.arange(m * k) % 17).astype(np.float32) - 8.0) * 0.02
+    wt = ((np.arange(n * k) % 13).astype(np.float32) - 6.0) * 0.02
+    return o.f32_to_bf16_trunc(x).reshape(m, k), o.f32_to_bf16_trunc(wt).reshape(n, k)
+
+
+@pytest.mark.parametrize("op", ["relu", "silu", "abs", "gelu", "neg"])
+def test_reference_epilogue_e2e_through_tile_abi(rt, bufs, op):
+    """test_epilogue_{relu,silu,abs}_gpu_e2e (src/t0/tile_ir.rs:5022-5225): 64x64x64
+    with the reference's patterned inputs, through lower_gemm's ABI (tile kernel +
+    build_kernargs_m + epilogue arguments + compute_grid + dispatch).  The reference's
+    own assertions (|err| <= 0.1 everywhere; ReLU zeroes every significant negative;
+    Abs leaves nothing negative) plus the north-star gate."""
+    m = k = n = 64
+    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    chain = t0g.epilogue_chain([op])
+    kern = rt.ensure_tile_kernel(cfg, epilogue_chain=chain)
+    x, wt = _reference_epilogue_inputs(m, k, n)
+    gemm_out = o.gemm("NT", x, wt, m, n, k)
+    expected = o.epilogue_chain(gemm_out, [op])
+    xa, wa = bufs.up(x), bufs.up(wt)
+    y = bufs.up(np.full((m, n), -9999.0, dtype=np.float32))
+    ka = t0g.build_kernargs_m_epilogue(xa, wa, y, k, n, m, cfg, chain)
+    rt.dispatch(kern, t0g.tile_compute_grid(cfg, m, n), ka)
+    got = rt.read(y, (m, n), np.float32)
+    assert np.abs(got - expected).max() <= 0.1
+    check_parity(got, expected, k, f"reference e2e {op}")
+    if op == "relu":
+        sig = gemm_out < -0.001
+        assert sig.any() and np.all(got[sig] < 0.001)
+    if op == "abs":
+        assert np.all(got >= 0.0)
+
+
+def test_tile_abi_chain_with_all_arguments(rt, bufs):
+    """Bias (at the unaligned offset 44), scale and clamp arguments read from the
+    tile kernargs, on a ragged NN problem."""
+    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(transpose=t0g.NN)
+    ops = ["bias", "scale", "silu", "clamp"]
+    chain = t0g.epilogue_chain(ops)
+    kern = rt.ensure_tile_kernel(cfg, epilogue_chain=chain)
+    m, k, n = 200, 192, 136
+    a = o.make_bf16_suite(m * k, 1).reshape(m, k)
+    b = o.make_bf16_suite(k * n, 2).reshape(k, n)
+    bias = (np.arange(n, dtype=np.float32) - 60.0) * 0.05
+    ref = o.epilogue_chain(o.gemm("NN", a, b, m, n, k), ops, bias=bias, scale=1.5, clamp=(-0.2, 0.9))
+    aa, ba, bb = bufs.up(a), bufs.up(b), bufs.up(bias)
+    y = bufs.up(np.full((m + 64, n), -9999.0, dtype=np.float32))
+    ka = t0g.build_kernargs_m_epilogue(aa, ba, y, k, n, m, cfg, chain, bias=bb, epi_scale=1.5, clamp=(-0.2, 0.9))
+    rt.dispatch(kern, t0g.tile_compute_grid(cfg, m, n), ka)
+    got = rt.read(y, (m + 64, n), np.float32)
+    check_parity(got[:m], ref, k, "tile ABI bias_scale_silu_clamp")
+    assert np.all(got[m:] == -9999.0)

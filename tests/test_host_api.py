@@ -171,3 +171,42 @@ def test_injected_hip_failure_maps_to_error():
         assert e.value.code == t0g.ERR_HIP and "failed" in str(e.value)
     finally:
         t0g.debug_fail_hip_call(0)
+
+
+def test_epilogue_chain_packing_names_and_kernargs():
+    """tile_ir EpilogueOp chains (src/t0/tile_ir.rs:41-62): packing, TileGemm::name's
+    epilogue tags (src/t0/tile_ir.rs:416-430) and lower_gemm's argument order after M
+    (bias, epi_scale, clamp_min, clamp_max; src/t0/tile_ir.rs:661-683)."""
+    c = t0g.epilogue_chain(["bias", "relu"])
+    assert c == t0g.OP_BIAS_ADD | (t0g.OP_RELU << 4)
+    assert t0g.epilogue_chain_name(c) == "_bias_relu"
+    assert t0g.epilogue_chain_name(0) == ""
+    assert t0g.epilogue_chain_name(t0g.epilogue_chain(["gelu", "neg", "abs", "clamp"])) == "_gelu_neg_abs_clamp"
+    with pytest.raises(t0g.T0gError):
+        t0g.epilogue_chain([9])
+    with pytest.raises(t0g.T0gError):
+        t0g.epilogue_chain(["relu"] * 9)
+    with pytest.raises(t0g.T0gError):
+        t0g.epilogue_chain_name(0x30)                 # a gap before an op
+    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    base = t0g.build_kernargs_m(1, 2, 3, 64, 32, 16, cfg)
+    ka = t0g.build_kernargs_m_epilogue(1, 2, 3, 64, 32, 16, cfg, t0g.epilogue_chain(["relu"]))
+    assert ka == base                                 # ReLU needs no arguments
+    chain = t0g.epilogue_chain(["bias", "scale", "clamp", "silu"])
+    ka = t0g.build_kernargs_m_epilogue(1, 2, 3, 64, 32, 16, cfg, chain, bias=0x1122334455667788,
+                                       epi_scale=0.5, clamp=(-2.0, 3.0))
+    assert len(ka) == 64 and ka[:44] == base
+    assert struct.unpack_from("<Qfff", ka, 44) == (0x1122334455667788, 0.5, -2.0, 3.0)
+    ka = t0g.build_kernargs_m_epilogue(1, 2, 3, 64, 32, 16, cfg, t0g.epilogue_chain(["clamp", "scale"]),
+                                       epi_scale=4.0, clamp=(0.0, 1.0))
+    assert len(ka) == 56 and struct.unpack_from("<fff", ka, 44) == (4.0, 0.0, 1.0)
+
+
+def test_desc_chain_validation():
+    d = t0g.gemm_desc(0x1000, 0x2000, 0x3000, 256, 256, 256, transpose="NN", epilogue_ops=["bias", "silu"])
+    with pytest.raises(t0g.T0gError) as e:             # BiasAdd without a bias pointer
+        t0g.gemm_kernel_name(d)
+    assert e.value.code == t0g.ERR_INVALID_ARG
+    d = t0g.gemm_desc(0x1000, 0x2000, 0x3000, 256, 256, 256, transpose="NN", epilogue_ops=["gelu", "clamp"],
+                      clamp=(-1.0, 1.0))
+    assert t0g.gemm_kernel_name(d).startswith("t0g_gemm_")

@@ -12,6 +12,7 @@ Each check is chosen so a plausible restatement mistake fails it:
   * bf16 rounding helpers are checked on IEEE tie cases; the PRNGs against an
     independent big-integer restatement and their documented ranges.
 """
+import math
 import os
 
 import numpy as np
@@ -204,3 +205,33 @@ def test_parity_gate_rejects_wrong_results():
     bad[3, 5] += 0.02
     assert not o.parity(bad, c, k)[0]
     assert not o.parity(c.T.copy(), c, k)[0]
+
+
+def test_epilogue_chain_known_answers():
+    """Each epilogue op against values fixed by the mathematics (not by retyping the
+    oracle's formulas): exact results for the piecewise ops, the identity
+    f(x) - f(-x) = x that any x * sigmoid(a x) satisfies, sigmoid's value at known
+    points computed in fp64, and chain order."""
+    x = np.array([[-3.0, -0.5, 0.0, 0.25, 2.0, 40.0, -40.0]], dtype=np.float32)
+    bias = np.array([1.0, 1.0, -1.0, 0.5, -4.0, 0.0, 0.0], dtype=np.float32)
+    assert np.array_equal(o.epilogue_chain(x, ["relu"]), [[0, 0, 0, 0.25, 2.0, 40.0, 0]])
+    assert np.array_equal(o.epilogue_chain(x, ["abs"]), np.abs(x))
+    assert np.array_equal(o.epilogue_chain(x, ["neg"]), -x)
+    assert np.array_equal(o.epilogue_chain(x, ["clamp"], clamp=(-1.0, 1.0)), [[-1, -0.5, 0, 0.25, 1, 1, -1]])
+    assert np.array_equal(o.epilogue_chain(x, ["scale"], scale=0.5), x * 0.5)
+    assert np.array_equal(o.epilogue_chain(x, ["bias"], bias=bias), x + bias)
+    # order matters: bias then ReLU is not ReLU then bias
+    assert np.array_equal(o.epilogue_chain(x, ["bias", "relu"], bias=bias), [[0, 0.5, 0, 0.75, 0, 40.0, 0]])
+    assert np.array_equal(o.epilogue_chain(x, ["relu", "bias"], bias=bias), [[1, 1, -1, 0.75, -2.0, 40.0, 0]])
+    # x*sigmoid(a x) - (-x)*sigmoid(-a x) = x for any a: pins the sign and the form
+    for op in ("silu", "gelu"):
+        f = o.epilogue_chain(x, [op]).astype(np.float64)
+        g = o.epilogue_chain(-x, [op]).astype(np.float64)
+        assert np.allclose(f - g, x, rtol=0, atol=2e-6), op
+    # values at x = 1 (fp64 sigmoid): silu(1) = 1/(1+e^-1), gelu(1) = 1/(1+e^-1.702)
+    one = np.ones((1, 1), dtype=np.float32)
+    assert abs(float(o.epilogue_chain(one, ["silu"])[0, 0]) - 1 / (1 + math.exp(-1.0))) < 1e-6
+    assert abs(float(o.epilogue_chain(one, ["gelu"])[0, 0]) - 1 / (1 + math.exp(-1.702))) < 1e-6
+    # saturation: large |x| gives x or 0, without NaN
+    s = o.epilogue_chain(x, ["silu"])
+    assert s[0, 5] == 40.0 and abs(s[0, 6]) < 1e-12 and np.isfinite(s).all()
