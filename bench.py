@@ -106,6 +106,49 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup):
             "kernels": [t0g.gemm_kernel_name(d) for d in descs]}
 
 
+def _event_ms(torch, stream, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def ignis_linear(torch, rt, stream, steps, warmup):
+    """The Ignis caller path on f32 device tensors (src/ignis/ops/bf16_matmul.rs): the
+    f32 -> bf16 conversion kernel alone (HBM-bound: 4 B read + 2 B written per element),
+    then a Linear layer of the MLP step (X [1024][4096] * W [4096][11008]) through
+    matmul (both operands converted on the GPU) and matmul_with_wt_bf16 (weight kept
+    as bf16, only X converted); f32 output."""
+    n_conv = 64 << 20
+    src = torch.randn(n_conv, device="cuda")
+    dst = torch.empty(n_conv, dtype=torch.bfloat16, device="cuda")
+    ms_conv = _event_ms(torch, stream, lambda: rt.f32_to_bf16(src.data_ptr(), dst.data_ptr(), n_conv), steps, warmup)
+    conv_gbs = 6.0 * n_conv / (ms_conv * 1e-3) / 1e9
+    del src, dst
+    m, k, n = 1024, 4096, 11008
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn((m, k), generator=g, device="cuda")
+    w = torch.randn((k, n), generator=g, device="cuda") * (2.0 / k) ** 0.5
+    wt16 = w.t().contiguous().to(torch.bfloat16)
+    y = torch.empty((m, n), device="cuda")
+    p = lambda t: t.data_ptr()
+    ms_mm = _event_ms(torch, stream, lambda: rt.matmul_f32(p(x), p(w), p(y), m, k, n), steps, warmup)
+    ms_wt = _event_ms(torch, stream, lambda: rt.matmul_wt_bf16_f32(p(x), p(wt16), p(y), m, k, n), steps, warmup)
+    flop = 2.0 * m * n * k
+    return {"f32_to_bf16_64Mi": {"ms": round(ms_conv, 4), "gbs": round(conv_gbs, 1),
+                                 "frac_of_hbm": round(conv_gbs / PEAK_GBS, 4)},
+            "matmul_f32_1024x4096x11008": {"ms": round(ms_mm, 4), "tflops": round(flop / (ms_mm * 1e-3) / 1e12, 2)},
+            "matmul_wt_bf16_f32_1024x4096x11008": {"ms": round(ms_wt, 4),
+                                                   "tflops": round(flop / (ms_wt * 1e-3) / 1e12, 2)}}
+
+
 def cpu_baseline(torch, tensors, m, n, k, min_seconds):
     """The CPU oracle (oracle/ref_gemm.c, a bit-exact restatement of the reference's
     CPU GEMM) on this host: the whole 4096^3 product, repeated to ~min_seconds."""
@@ -260,6 +303,8 @@ def main():
         log("[bench] MLP step")
         extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
                                                      max(2, args.warmup // 10))
+        log("[bench] Ignis f32 caller path")
+        extra["ignis"] = ignis_linear(torch, rt, stream, max(5, args.steps // 2), max(3, args.warmup // 4))
         line["extra"] = extra
 
     if args.cpu_seconds > 0:

@@ -271,6 +271,35 @@ T0G_API int t0g_gemm_workspace_size(const t0g_gemm_desc *desc, size_t *bytes);
 /* Name of the gfx950 kernel symbol t0g_gemm would launch for desc. */
 T0G_API int t0g_gemm_kernel_name(const t0g_gemm_desc *desc, char *buf, size_t len);
 
+/* ---- Ignis bf16_matmul caller path on f32 device tensors ------------------- *
+ * src/ignis/ops/bf16_matmul.rs converts its f32 operands to bf16 on the CPU,
+ * transposes and pads them there, runs an NT GEMM and unpads the result with a
+ * second kernel.  Here the conversion runs on the GPU (t0g_f32_to_bf16, the
+ * same rounding) into a library-managed scratch buffer, and the GEMM uses the
+ * layout the operands already have (NN / NT / TN), unpadded: Y is written at
+ * its final [rows][cols] stride.  All pointers are device addresses of packed
+ * row-major arrays; the calls are asynchronous on the device stream. */
+
+/* f32 -> bf16, RNE as (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16
+ * (src/ignis/ops/bf16_matmul.rs:372-375, no NaN special case). */
+T0G_API int t0g_f32_to_bf16(t0g_device *dev, uint64_t src_f32, uint64_t dst_bf16, size_t n);
+/* bf16_matmul::matmul forward (src/ignis/ops/bf16_matmul.rs:33-56, 160-211):
+ * Y[M,N] = bf16(X[M,K]) * bf16(W[K,N]), f32 accumulate and output. */
+T0G_API int t0g_matmul_f32(t0g_device *dev, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k,
+                           uint32_t n);
+/* gemm_backward_data (src/ignis/ops/bf16_matmul.rs:215-260):
+ * dX[M,K] = bf16(dY[M,N]) * bf16(W[K,N])^T. */
+T0G_API int t0g_matmul_backward_data_f32(t0g_device *dev, uint64_t dy, uint64_t w, uint64_t dx, uint32_t m,
+                                         uint32_t k, uint32_t n);
+/* gemm_backward_weight (src/ignis/ops/bf16_matmul.rs:265-308):
+ * dW[K,N] = bf16(X[M,K])^T * bf16(dY[M,N]). */
+T0G_API int t0g_matmul_backward_weight_f32(t0g_device *dev, uint64_t x, uint64_t dy, uint64_t dw, uint32_t m,
+                                           uint32_t k, uint32_t n);
+/* matmul_with_wt_bf16 (src/ignis/ops/bf16_matmul.rs:98-133): Y[M,N] =
+ * bf16(X[M,K]) * WT[N,K]^T with WT already bf16. */
+T0G_API int t0g_matmul_wt_bf16_f32(t0g_device *dev, uint64_t x, uint64_t wt_bf16, uint64_t y, uint32_t m,
+                                   uint32_t k, uint32_t n);
+
 /* ---- test hooks ------------------------------------------------------------ */
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a

@@ -1061,6 +1061,39 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
 
 }  // namespace t0g
 
+// f32 -> bf16 with the rounding of the reference's operand conversion
+// (src/ignis/ops/bf16_matmul.rs:372-375): (bits + 0x7FFF + ((bits >> 16) & 1)) >> 16,
+// integer arithmetic, no special case for NaN.  HBM-bound: 6 bytes per element.
+namespace t0g {
+__device__ __forceinline__ uint32_t bf16_bits_ref(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+}  // namespace t0g
+
+extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvertArgs p) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    const uint64_t stride = (uint64_t)p.grid_blocks * 256;
+    if (p.flags & T0G_CONVERT_VEC) {
+        const uint64_t n8 = p.n >> 3;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+            const __attribute__((address_space(1))) f32x4_t* s =
+                reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>((uintptr_t)p.src) + 2 * i;
+            const f32x4_t lo = __builtin_nontemporal_load(s), hi = __builtin_nontemporal_load(s + 1);
+            u32x4_t w;
+            w[0] = t0g::bf16_bits_ref(lo[0]) | (t0g::bf16_bits_ref(lo[1]) << 16);
+            w[1] = t0g::bf16_bits_ref(lo[2]) | (t0g::bf16_bits_ref(lo[3]) << 16);
+            w[2] = t0g::bf16_bits_ref(hi[0]) | (t0g::bf16_bits_ref(hi[1]) << 16);
+            w[3] = t0g::bf16_bits_ref(hi[2]) | (t0g::bf16_bits_ref(hi[3]) << 16);
+            reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)p.dst)[i] = w;
+        }
+        return;
+    }
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < p.n; i += stride)
+        reinterpret_cast<__attribute__((address_space(1))) uint16_t*>((uintptr_t)p.dst)[i] =
+            (uint16_t)t0g::bf16_bits_ref(reinterpret_cast<const __attribute__((address_space(1))) float*>((uintptr_t)p.src)[i]);
+}
+
 // ---------------------------------------------------------------------------
 // Exported kernel symbols (looked up by name with hipModuleGetFunction).
 // t0g_gemm_<BM>x<BN>_k64_<layout>_<out>[_u]   (_u: element-wise loads for

@@ -44,11 +44,20 @@ typedef struct T0gReduceArgs {
     uint32_t reserved;
 } T0gReduceArgs;
 
+typedef struct T0gConvertArgs {
+    uint64_t src;            /* f32 [n]                                           */
+    uint64_t dst;            /* bf16 [n]                                          */
+    uint64_t n;              /* elements                                          */
+    uint32_t grid_blocks;    /* launched workgroups (256 threads each)           */
+    uint32_t flags;          /* T0G_CONVERT_VEC                                   */
+} T0gConvertArgs;
+
 #define T0G_FLAG_XCD_REMAP 1u   /* remap block ids so each XCD owns a contiguous tile range */
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
 #define T0G_FLAG_BIAS 4u        /* the chain reads bias[col]                                     */
 #define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
 #define T0G_REDUCE_BIAS 2u      /* the chain reads bias[col]                                     */
+#define T0G_CONVERT_VEC 1u      /* src 32-byte and dst 16-byte aligned: 8 elements per step      */
 
 /* Epilogue chain operations: tile_ir's EpilogueOp (src/t0/tile_ir.rs:41-62),
  * applied in chain order to each fp32 result before the output conversion. */

@@ -70,6 +70,8 @@ struct t0g_device {
     std::set<uint64_t> allocations;
     uint64_t ws = 0;
     size_t ws_bytes = 0;
+    uint64_t conv = 0;         // bf16 operand scratch of the matmul entry points
+    size_t conv_bytes = 0;
 };
 
 namespace t0g {
@@ -445,6 +447,7 @@ int t0g_device_close(t0g_device *dev) {
     (void)hipSetDevice(dev->ordinal);
     if (!dev->poisoned) (void)hipStreamSynchronize(dev->stream);
     if (dev->ws) (void)hipFree((void *)dev->ws);
+    if (dev->conv) (void)hipFree((void *)dev->conv);
     for (uint64_t a : dev->allocations) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
@@ -791,14 +794,13 @@ int t0g_gemm_kernel_name(const t0g_gemm_desc *d, char *buf, size_t len) {
     return ok();
 }
 
-int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
-    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+// t0g_gemm with dev->mu held.
+static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d) {
     t0g_gemm_config cfg;
     GemmPlan p;
     GemmOperands o;
     int rc = resolve_desc(d, &cfg, &p, &o);
     if (rc) return rc;
-    std::lock_guard<std::mutex> lk(dev->mu);
     if ((rc = check_usable(dev))) return rc;
     if (d->m == 0 || d->n == 0) return ok();
     uint64_t ws = 0;
@@ -816,6 +818,114 @@ int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
     }
     if ((rc = run_plan(dev, p, o, ws))) return rc;
     return ok();
+}
+
+int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    return gemm_locked(dev, d);
+}
+
+// ---- Ignis bf16_matmul caller path ------------------------------------------
+
+static int convert_locked(t0g_device *dev, uint64_t src, uint64_t dst, uint64_t n) {
+    if (n == 0) return T0G_OK;
+    hipFunction_t f = nullptr;
+    int rc = get_function(dev, "t0g_f32_to_bf16_rne", &f);
+    if (rc) return rc;
+    T0gConvertArgs a;
+    memset(&a, 0, sizeof a);
+    a.src = src;
+    a.dst = dst;
+    a.n = n;
+    const bool vec = (src & 31) == 0 && (dst & 15) == 0 && (n & 7) == 0;
+    if (vec) a.flags |= T0G_CONVERT_VEC;
+    uint64_t blocks = ((vec ? n / 8 : n) + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    a.grid_blocks = (uint32_t)blocks;
+    return launch(dev, f, (uint32_t)blocks, 1, 1, 256, &a, sizeof a);
+}
+
+static int ensure_conv(t0g_device *dev, size_t bytes) {
+    if (dev->conv_bytes >= bytes) return T0G_OK;
+    if (dev->conv) {
+        hipError_t e = T0G_HIP(hipFree((void *)dev->conv));   // waits for work using it
+        dev->conv = 0;
+        dev->conv_bytes = 0;
+        if (e != hipSuccess) return poison(dev, hip_fail(e, "hipFree(conversion scratch)"));
+    }
+    void *p = nullptr;
+    hipError_t e = T0G_HIP(hipMalloc(&p, bytes));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(conversion scratch)");
+    dev->conv = (uint64_t)p;
+    dev->conv_bytes = bytes;
+    return T0G_OK;
+}
+
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Convert the f32 operands that need it into the scratch buffer, then run one
+// GEMM with f32 output.  a_elems / b_elems: elements of A and B (0: already bf16).
+static int matmul_common(t0g_device *dev, uint64_t a_f32, size_t a_elems, uint64_t b, size_t b_elems,
+                         uint64_t c, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    if (!a_f32 || !b || !c) return fail(T0G_ERR_INVALID_ARG, "NULL operand");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    const size_t a_bytes = round256(a_elems * 2), b_bytes = round256(b_elems * 2);
+    if ((rc = ensure_conv(dev, a_bytes + b_bytes + 256))) return rc;
+    const uint64_t a16 = dev->conv, b16 = b_elems ? dev->conv + a_bytes : b;
+    if ((rc = convert_locked(dev, a_f32, a16, a_elems))) return rc;
+    if (b_elems && (rc = convert_locked(dev, b, b16, b_elems))) return rc;
+    t0g_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = a16;
+    d.b = b16;
+    d.c = c;
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.transpose = transpose;
+    d.out_dtype = T0G_F32;
+    return gemm_locked(dev, &d);
+}
+
+int t0g_f32_to_bf16(t0g_device *dev, uint64_t src, uint64_t dst, size_t n) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    if (n && (!src || !dst)) return fail(T0G_ERR_INVALID_ARG, "NULL buffer");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if ((rc = convert_locked(dev, src, dst, n))) return rc;
+    return ok();
+}
+
+int t0g_matmul_f32(t0g_device *dev, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k, uint32_t n) {
+    // Y = X * W: X [M][K] is K-contiguous, W [K][N] is N-contiguous -> NN.
+    int rc = matmul_common(dev, x, (size_t)m * k, w, (size_t)k * n, y, m, n, k, T0G_NN);
+    return rc ? rc : ok();
+}
+
+int t0g_matmul_backward_data_f32(t0g_device *dev, uint64_t dy, uint64_t w, uint64_t dx, uint32_t m, uint32_t k,
+                                 uint32_t n) {
+    // dX[M,K] = dY[M,N] * W[K,N]^T: contraction over N; dY rows and W rows are N-contiguous -> NT.
+    int rc = matmul_common(dev, dy, (size_t)m * n, w, (size_t)k * n, dx, m, k, n, T0G_NT);
+    return rc ? rc : ok();
+}
+
+int t0g_matmul_backward_weight_f32(t0g_device *dev, uint64_t x, uint64_t dy, uint64_t dw, uint32_t m, uint32_t k,
+                                   uint32_t n) {
+    // dW[K,N] = X[M,K]^T * dY[M,N]: contraction over M; both operands are M-major -> TN.
+    int rc = matmul_common(dev, x, (size_t)m * k, dy, (size_t)m * n, dw, k, n, m, T0G_TN);
+    return rc ? rc : ok();
+}
+
+int t0g_matmul_wt_bf16_f32(t0g_device *dev, uint64_t x, uint64_t wt_bf16, uint64_t y, uint32_t m, uint32_t k,
+                           uint32_t n) {
+    // Y = X * WT^T with WT [N][K] bf16 -> NT; only X needs converting.
+    int rc = matmul_common(dev, x, (size_t)m * k, wt_bf16, 0, y, m, n, k, T0G_NT);
+    return rc ? rc : ok();
 }
 
 }  // extern "C"

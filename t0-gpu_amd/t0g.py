@@ -200,6 +200,11 @@ _sig("t0g_wait_idle", ctypes.c_int, _p)
 _sig("t0g_gemm", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
 _sig("t0g_gemm_workspace_size", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_gemm_kernel_name", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_f32_to_bf16", ctypes.c_int, _p, _u64, _u64, ctypes.c_size_t)
+_sig("t0g_matmul_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
+_sig("t0g_matmul_backward_data_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
+_sig("t0g_matmul_backward_weight_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
+_sig("t0g_matmul_wt_bf16_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 
@@ -511,3 +516,23 @@ class GpuRuntime:
     def gemm(self, a, b, c, m, n, k, **kw):
         """Enqueue C = op(A) op(B) on the device stream (asynchronous)."""
         self.gemm_desc(gemm_desc(a, b, c, m, n, k, **kw))
+
+    # Ignis bf16_matmul caller path (src/ignis/ops/bf16_matmul.rs) on f32 device tensors
+    def f32_to_bf16(self, src, dst, n):
+        _check(_lib.t0g_f32_to_bf16(self.handle, src, dst, n))
+
+    def matmul_f32(self, x, w, y, m, k, n):
+        """bf16_matmul::matmul forward: Y[M,N] = bf16(X[M,K]) bf16(W[K,N])."""
+        _check(_lib.t0g_matmul_f32(self.handle, x, w, y, m, k, n))
+
+    def matmul_backward_data_f32(self, dy, w, dx, m, k, n):
+        """gemm_backward_data: dX[M,K] = bf16(dY[M,N]) bf16(W[K,N])^T."""
+        _check(_lib.t0g_matmul_backward_data_f32(self.handle, dy, w, dx, m, k, n))
+
+    def matmul_backward_weight_f32(self, x, dy, dw, m, k, n):
+        """gemm_backward_weight: dW[K,N] = bf16(X[M,K])^T bf16(dY[M,N])."""
+        _check(_lib.t0g_matmul_backward_weight_f32(self.handle, x, dy, dw, m, k, n))
+
+    def matmul_wt_bf16_f32(self, x, wt_bf16, y, m, k, n):
+        """matmul_with_wt_bf16: Y[M,N] = bf16(X[M,K]) WT[N,K]^T."""
+        _check(_lib.t0g_matmul_wt_bf16_f32(self.handle, x, wt_bf16, y, m, k, n))

@@ -614,3 +614,103 @@ def test_tile_abi_chain_with_all_arguments(rt, bufs):
     got = rt.read(y, (m + 64, n), np.float32)
     check_parity(got[:m], ref, k, "tile ABI bias_scale_silu_clamp")
     assert np.all(got[m:] == -9999.0)
+
+
+# ---- Ignis bf16_matmul caller path (src/ignis/ops/bf16_matmul.rs) ----------
+def test_f32_to_bf16_is_the_reference_rounding(rt, bufs):
+    """GPU conversion = the reference's integer RNE (bf16_matmul.rs:372-375), bit for
+    bit, including ties, infinities, denormals and a NaN that the formula turns into
+    -0.0 (it has no NaN special case); vector and scalar paths, aligned and not."""
+    rng = np.random.default_rng(5)
+    special = np.array([0x3F808000, 0x3F818000, 0x3F80FFFF, 0x7F7FFFFF, 0x7F800000, 0xFF800000,
+                        0x00000001, 0x807FFFFF, 0x7FC00000, 0x7FFFFFFF, 0x00000000, 0x80000000],
+                       dtype=np.uint32)
+    for n in (1 << 20, 1000003):
+        bits = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+        bits[:special.size] = special
+        x = bits.view(np.float32)
+        for off in (0, 1):                            # off = 1: unaligned source, scalar path
+            src = bufs.up(np.concatenate([np.zeros(off, np.float32), x]))
+            dst = bufs.alloc(2 * n + 64, fill=0)
+            rt.f32_to_bf16(src + 4 * off, dst, n)
+            rt.wait_idle()
+            got = rt.read(dst, (n,), np.uint16)
+            assert np.array_equal(got, o.f32_to_bf16_rne(x)), f"n={n} off={off}"
+    assert o.f32_to_bf16_rne(np.array([0x7FFFFFFF], np.uint32).view(np.float32))[0] == 0x8000
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4, 2), (64, 256, 512), (100, 300, 72), (1024, 4096, 1104)])
+def test_ignis_matmul_forward_and_backward(rt, bufs, m, k, n):
+    """matmul / gemm_backward_data / gemm_backward_weight / matmul_with_wt_bf16
+    (src/ignis/ops/bf16_matmul.rs:33-308) on f32 device tensors: GPU conversion, native
+    layouts, no padding; against the oracle on the RNE-converted operands."""
+    rng = np.random.default_rng(m * 7 + n)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w = rng.standard_normal((k, n), dtype=np.float32) * 0.1
+    dy = rng.standard_normal((m, n), dtype=np.float32)
+    x16, w16, dy16 = o.f32_to_bf16_rne(x), o.f32_to_bf16_rne(w), o.f32_to_bf16_rne(dy)
+    xa, wa, dya = bufs.up(x), bufs.up(w), bufs.up(dy)
+    y, dx, dw, y2 = (bufs.alloc(4 * s, fill=0) for s in (m * n, m * k, k * n, m * n))
+    rt.matmul_f32(xa, wa, y, m, k, n)
+    rt.matmul_backward_data_f32(dya, wa, dx, m, k, n)
+    rt.matmul_backward_weight_f32(xa, dya, dw, m, k, n)
+    wt16 = bufs.up(np.ascontiguousarray(w16.reshape(k, n).T))
+    rt.matmul_wt_bf16_f32(xa, wt16, y2, m, k, n)
+    rt.wait_idle()
+    check_parity(rt.read(y, (m, n), np.float32), o.gemm("NN", x16.reshape(m, k), w16.reshape(k, n), m, n, k),
+                 k, f"matmul {m}x{k}x{n}")
+    check_parity(rt.read(dx, (m, k), np.float32), o.gemm("NT", dy16.reshape(m, n), w16.reshape(k, n), m, k, n),
+                 n, "backward data")
+    check_parity(rt.read(dw, (k, n), np.float32), o.gemm("TN", x16.reshape(m, k), dy16.reshape(m, n), k, n, m),
+                 m, "backward weight")
+    assert np.array_equal(rt.read(y2, (m, n), np.float32), rt.read(y, (m, n), np.float32))
+
+
+def test_linear_forward_reference_case(rt, bufs):
+    """test_linear_forward (src/ignis/tests.rs:304-311): Linear::new(4, 2) (He-init LCG,
+    seed 42, src/ignis/nn/linear.rs:36-43) applied to ones[1, 4] gives a [1, 2] output,
+    here also checked against the oracle value."""
+    w = o.linear_init_f32(4, 2)
+    x = np.ones((1, 4), dtype=np.float32)
+    xa, wa = bufs.up(x), bufs.up(w)
+    y = bufs.alloc(8, fill=0)
+    rt.matmul_f32(xa, wa, y, 1, 4, 2)
+    rt.wait_idle()
+    got = rt.read(y, (1, 2), np.float32)
+    ref = o.gemm("NN", o.f32_to_bf16_rne(x).reshape(1, 4), o.f32_to_bf16_rne(w).reshape(4, 2), 1, 2, 4)
+    assert got.shape == (1, 2)
+    check_parity(got, ref, 4, "linear forward 1x4x2")
+
+
+def test_linear_regression_training_reduces_loss(rt, bufs):
+    """In the spirit of test_e2e_training (src/ignis/tests.rs:396-480): gradient flow
+    through the GPU matmul forward and weight backward; 20 plain SGD steps (lr 2.0, below
+    2/L for this least-squares problem) must cut the loss below a tenth, and the first
+    gradient must match the oracle."""
+    m, k, n = 64, 32, 16
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    w_true = rng.standard_normal((k, n), dtype=np.float32) * 0.5
+    t = x @ w_true
+    w = o.linear_init_f32(k, n)
+    xa = bufs.up(x)
+    wa = bufs.alloc(4 * k * n)
+    y, dya, dw = bufs.alloc(4 * m * n), bufs.alloc(4 * m * n), bufs.alloc(4 * k * n)
+    losses = []
+    for step in range(20):
+        rt.write(wa, w)
+        rt.matmul_f32(xa, wa, y, m, k, n)
+        rt.wait_idle()
+        pred = rt.read(y, (m, n), np.float32)
+        diff = pred - t
+        losses.append(float(np.mean(diff * diff)))
+        g_out = (2.0 / diff.size) * diff
+        rt.write(dya, g_out.astype(np.float32))
+        rt.matmul_backward_weight_f32(xa, dya, dw, m, k, n)
+        rt.wait_idle()
+        g = rt.read(dw, (k, n), np.float32)
+        if step == 0:
+            ref = o.gemm("TN", o.f32_to_bf16_rne(x), o.f32_to_bf16_rne(g_out.astype(np.float32)), k, n, m)
+            check_parity(g, ref, m, "dW step 0")
+        w = w - 2.0 * g
+    assert losses[-1] < losses[0] * 0.1, losses
