@@ -36,12 +36,13 @@ def make_inputs(torch, m, n, k, layout, seed):
     return a, b
 
 
-def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None, epilogue_ops=None):
+def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None, epilogue_ops=None,
+              config=None):
     a, b = make_inputs(torch, m, n, k, layout, seed)
     c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
     bias = torch.linspace(-1.0, 1.0, n, device="cuda", dtype=torch.float32)
     desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16,
-                         epilogue_ops=epilogue_ops, bias=bias.data_ptr() if epilogue_ops else 0)
+                         epilogue_ops=epilogue_ops, bias=bias.data_ptr() if epilogue_ops else 0, config=config)
     kname = t0g.gemm_kernel_name(desc)
     for _ in range(warmup):
         rt.gemm_desc(desc)
@@ -63,9 +64,14 @@ def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, ou
     return res
 
 
-def mlp_step(t0g, torch, rt, stream, steps, warmup):
+MLP_SHAPES = [("NN", 1024, 11008, 4096), ("NN", 1024, 4096, 11008), ("NT", 1024, 11008, 4096),
+              ("NT", 1024, 4096, 11008), ("TN", 11008, 4096, 1024), ("TN", 4096, 11008, 1024)]
+
+
+def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None):
     """forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
-    dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out."""
+    dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out.  configs: one
+    GemmConfig per GEMM (in MLP_SHAPES order) instead of auto_select's."""
     bsz, d_in, d_hid = 1024, 4096, 11008
     g = torch.Generator(device="cuda").manual_seed(7)
     x = torch.randn((bsz, d_in), generator=g, device="cuda").to(torch.bfloat16)
@@ -79,13 +85,14 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup):
     dw1 = torch.empty_like(w1)
     dw2 = torch.empty_like(w2)
     p = lambda t: t.data_ptr()
+    cf = configs or [None] * 6
     descs = [
-        t0g.gemm_desc(p(x), p(w1), p(h), bsz, d_hid, d_in, transpose="NN", out_dtype=t0g.BF16),
-        t0g.gemm_desc(p(h), p(w2), p(y), bsz, d_in, d_hid, transpose="NN", out_dtype=t0g.BF16),
-        t0g.gemm_desc(p(dy), p(w2), p(dh), bsz, d_hid, d_in, transpose="NT", out_dtype=t0g.BF16),
-        t0g.gemm_desc(p(dh), p(w1), p(dx), bsz, d_in, d_hid, transpose="NT", out_dtype=t0g.BF16),
-        t0g.gemm_desc(p(h), p(dy), p(dw2), d_hid, d_in, bsz, transpose="TN", out_dtype=t0g.BF16),
-        t0g.gemm_desc(p(x), p(dh), p(dw1), d_in, d_hid, bsz, transpose="TN", out_dtype=t0g.BF16),
+        t0g.gemm_desc(p(x), p(w1), p(h), bsz, d_hid, d_in, transpose="NN", out_dtype=t0g.BF16, config=cf[0]),
+        t0g.gemm_desc(p(h), p(w2), p(y), bsz, d_in, d_hid, transpose="NN", out_dtype=t0g.BF16, config=cf[1]),
+        t0g.gemm_desc(p(dy), p(w2), p(dh), bsz, d_hid, d_in, transpose="NT", out_dtype=t0g.BF16, config=cf[2]),
+        t0g.gemm_desc(p(dh), p(w1), p(dx), bsz, d_in, d_hid, transpose="NT", out_dtype=t0g.BF16, config=cf[3]),
+        t0g.gemm_desc(p(h), p(dy), p(dw2), d_hid, d_in, bsz, transpose="TN", out_dtype=t0g.BF16, config=cf[4]),
+        t0g.gemm_desc(p(x), p(dh), p(dw1), d_in, d_hid, bsz, transpose="TN", out_dtype=t0g.BF16, config=cf[5]),
     ]
     for _ in range(warmup):
         for d in descs:
@@ -147,6 +154,44 @@ def ignis_linear(torch, rt, stream, steps, warmup):
             "matmul_f32_1024x4096x11008": {"ms": round(ms_mm, 4), "tflops": round(flop / (ms_mm * 1e-3) / 1e12, 2)},
             "matmul_wt_bf16_f32_1024x4096x11008": {"ms": round(ms_wt, 4),
                                                    "tflops": round(flop / (ms_wt * 1e-3) / 1e12, 2)}}
+
+
+def tuner_extra(t0g, torch, rt, stream, steps, warmup):
+    """GemmTuner (src/t0/auto_gemm.rs) on the BASELINE shapes, from an empty cache: the
+    tuning time, a cache hit's time, and each shape's GEMM with auto_select's config
+    and with the tuned one (same harness as the other lines); then the MLP step with
+    the tuned configs."""
+    import tempfile
+    shapes = [("NT", 128, 4096, 4096), ("NT", 256, 256, 32768), ("NN", 4096, 4096, 4096)] + MLP_SHAPES
+    out = {}
+    tuned = {}
+    with tempfile.TemporaryDirectory() as d, t0g.GemmTuner.with_cache_dir(d) as tuner:
+        rt.set_stream(None)   # the tuner synchronises the library's own stream
+        t_tune = 0.0
+        for lay, m, n, k in shapes:
+            t0 = time.perf_counter()
+            cfg = tuner.tune(rt, m, n, k, transpose=lay, out_dtype=t0g.BF16)
+            t_tune += time.perf_counter() - t0
+            tuned[(lay, m, n, k)] = cfg
+        t0 = time.perf_counter()
+        for lay, m, n, k in shapes:
+            tuner.tune(rt, m, n, k, transpose=lay, out_dtype=t0g.BF16)
+        t_hit = (time.perf_counter() - t0) / len(shapes)
+        rt.set_stream(stream.cuda_stream)
+        out["tuning_s_total"] = round(t_tune, 3)
+        out["cache_hit_us"] = round(t_hit * 1e6, 2)
+        for lay, m, n, k in shapes:
+            cfg = tuned[(lay, m, n, k)]
+            auto = t0g.auto_select(m, k, n)
+            ra = time_gemm(t0g, torch, rt, stream, m, n, k, lay, steps, warmup, seed=13)
+            rtu = time_gemm(t0g, torch, rt, stream, m, n, k, lay, steps, warmup, seed=13, config=cfg)
+            out[f"{lay.lower()}_{m}x{n}x{k}"] = {
+                "auto_select": auto.name(), "auto_us": round(ra["event_ms_per_launch"] * 1e3, 2),
+                "tuned": cfg.name(), "tuned_us": round(rtu["event_ms_per_launch"] * 1e3, 2),
+                "tuned_tflops": round(rtu["flop"] / (rtu["event_ms_per_launch"] * 1e-3) / 1e12, 1)}
+    out["mlp_step_tuned"] = mlp_step(t0g, torch, rt, stream, max(3, steps // 5), max(2, warmup // 10),
+                                     configs=[tuned[s] for s in MLP_SHAPES])
+    return out
 
 
 def cpu_baseline(torch, tensors, m, n, k, min_seconds):
@@ -303,6 +348,8 @@ def main():
         log("[bench] MLP step")
         extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
                                                      max(2, args.warmup // 10))
+        log("[bench] GemmTuner on the BASELINE shapes")
+        extra["tuner"] = tuner_extra(t0g, torch, rt, stream, max(10, args.steps // 2), max(10, args.warmup // 4))
         log("[bench] Ignis f32 caller path")
         extra["ignis"] = ignis_linear(torch, rt, stream, max(5, args.steps // 2), max(3, args.warmup // 4))
         line["extra"] = extra

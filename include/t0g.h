@@ -300,6 +300,74 @@ T0G_API int t0g_matmul_backward_weight_f32(t0g_device *dev, uint64_t x, uint64_t
 T0G_API int t0g_matmul_wt_bf16_f32(t0g_device *dev, uint64_t x, uint64_t wt_bf16, uint64_t y, uint32_t m,
                                    uint32_t k, uint32_t n);
 
+/* ---- GEMM autotuner and its on-disk cache ----------------------------------- *
+ * GemmTuner (src/t0/auto_gemm.rs:28-417): benchmark the model's best candidate
+ * configs on the GPU, keep the fastest, cache it in memory and as one JSON file
+ * per problem under the cache directory (default $HOME/.t0_autotune, else
+ * /tmp/.t0_autotune; auto_gemm.rs:484-490).  Files keep the reference's keys
+ * (tile_m, tile_n, tile_k, wg_size, split_k, lds_pad, n_col_passes, wgp, swap,
+ * tflops, all; auto_gemm.rs:364-391) and add "arch":"gfx950", the layout, the
+ * output type and the problem size; a file without "arch":"gfx950" (one the
+ * gfx1100 build wrote) or whose config is not valid here counts as a miss and
+ * is re-tuned.  The key is (M, N, K, layout, output type); NT with f32 output
+ * uses the reference's file name gemm_MxNxK.json, other keys add a suffix. */
+typedef struct t0g_tuner t0g_tuner;
+
+/* GemmTuneResult (src/t0/auto_gemm.rs:28-42); `all` is read with
+ * t0g_tuner_ranking. */
+typedef struct t0g_tune_result {
+    t0g_gemm_config best;       /* best->transpose = layout tuned for */
+    double best_tflops;
+    uint32_t m, n, k;           /* key, in the reference's (M, N, K) order */
+    uint32_t transpose;         /* t0g_transpose */
+    uint32_t out_dtype;         /* t0g_dtype */
+    int32_t from_cache;         /* 1: loaded from disk, 0: measured in this process */
+    uint32_t n_all;             /* entries in the ranking */
+    uint32_t reserved;
+} t0g_tune_result;
+
+/* GemmTuner::new / with_cache_dir (auto_gemm.rs:59-75); cache_dir NULL or "" =
+ * the default.  max_candidates 8, n_iters 5. */
+T0G_API int t0g_tuner_create(const char *cache_dir, t0g_tuner **out);
+T0G_API int t0g_tuner_destroy(t0g_tuner *tuner);
+/* global_tuner() (auto_gemm.rs:429-431): one process-wide tuner with the default directory. */
+T0G_API int t0g_tuner_global(t0g_tuner **out);
+T0G_API int t0g_tuner_set_params(t0g_tuner *tuner, uint32_t max_candidates, uint32_t n_iters);
+T0G_API int t0g_tuner_get_params(t0g_tuner *tuner, uint32_t *max_candidates, uint32_t *n_iters,
+                                 uint32_t *n_cached);
+T0G_API int t0g_tuner_cache_dir(t0g_tuner *tuner, char *buf, size_t len);
+/* The candidate list tune() benchmarks (auto_gemm.rs:107-112: the cost model's
+ * best first): every MI355X tile x split_k in order of modelled time, at most
+ * max entries.  Host only. */
+T0G_API int t0g_tune_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t max,
+                                t0g_gemm_config *out, uint32_t *count);
+/* GemmTuner::tune(rt, m, n, k) (auto_gemm.rs:82-163): memory, then disk, then
+ * benchmark (random bf16 operands, device time by HIP events, median of n_iters
+ * after ~10 ms of warm-up launches per candidate) and persist.  Synchronous. */
+T0G_API int t0g_tuner_tune(t0g_tuner *tuner, t0g_device *dev, uint32_t m, uint32_t n, uint32_t k,
+                           uint32_t transpose, uint32_t out_dtype, t0g_gemm_config *best);
+/* Cached result without benchmarking: *found = 0 on a miss. */
+T0G_API int t0g_tuner_lookup(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                             uint32_t out_dtype, t0g_tune_result *out, int *found);
+/* Entry i of the ranking of a cached result (fastest first). */
+T0G_API int t0g_tuner_ranking(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                              uint32_t out_dtype, uint32_t i, char *name, size_t name_len, double *tflops);
+/* save_cache (auto_gemm.rs:364-391) of a result and its ranking, also into
+ * memory; names[i] / tflops[i] for i < n_all. */
+T0G_API int t0g_tuner_store(t0g_tuner *tuner, const t0g_tune_result *result, const char *const *names,
+                            const double *tflops, uint32_t n_all);
+/* invalidate / clear (auto_gemm.rs:393-403). */
+T0G_API int t0g_tuner_invalidate(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
+                                 uint32_t out_dtype);
+T0G_API int t0g_tuner_clear(t0g_tuner *tuner);
+/* report (auto_gemm.rs:405-417) into buf; *needed = bytes including the NUL. */
+T0G_API int t0g_tuner_report(t0g_tuner *tuner, char *buf, size_t len, size_t *needed);
+/* auto_gemm(rt, a, b, c, m, n, k) (auto_gemm.rs:445-480): tune (NT, f32 out,
+ * tuner NULL = the global one), then enqueue C[M][N] = A[M][K] * B[N][K]^T with
+ * the best config; *tflops (may be NULL) = the cached measurement. */
+T0G_API int t0g_auto_gemm(t0g_tuner *tuner, t0g_device *dev, uint64_t a, uint64_t b, uint64_t c, uint32_t m,
+                          uint32_t n, uint32_t k, double *tflops);
+
 /* ---- test hooks ------------------------------------------------------------ */
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a

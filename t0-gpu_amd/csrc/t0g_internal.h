@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "t0g.h"
 
@@ -47,6 +48,10 @@ uint32_t legacy_chain(uint32_t epilogue);          // t0g_epilogue -> chain
 int check_chain(uint32_t chain);                   // codes valid, no gaps
 bool chain_has(uint32_t chain, uint32_t op);
 uint32_t chain_kernarg_bytes(uint32_t chain);      // tile_ir arguments after M
+
+// Device time (ms) of each of `iters` t0g_gemm launches of d, after `warmup`
+// untimed ones (t0g_runtime.cpp).
+int time_gemm(t0g_device *dev, const t0g_gemm_desc *d, uint32_t warmup, uint32_t iters, std::vector<double> *ms);
 
 }  // namespace t0g
 

@@ -826,6 +826,55 @@ int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
     return gemm_locked(dev, d);
 }
 
+}  // extern "C"
+
+namespace t0g {
+
+// Device time of `iters` back-to-back t0g_gemm launches of d (after `warmup`
+// untimed ones): one HIP event between consecutive launches on the device
+// stream, so each duration covers one whole GEMM (partials and reduce).
+int time_gemm(t0g_device *dev, const t0g_gemm_desc *d, uint32_t warmup, uint32_t iters, std::vector<double> *ms) {
+    if (!dev || !d || !ms || iters == 0) return fail(T0G_ERR_INVALID_ARG, "time_gemm: bad argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    std::vector<hipEvent_t> ev(iters + 1, nullptr);
+    auto destroy = [&ev]() {
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+    };
+    for (hipEvent_t &e : ev) {
+        hipError_t he = T0G_HIP(hipEventCreate(&e));
+        if (he != hipSuccess) {
+            e = nullptr;
+            destroy();
+            return hip_fail(he, "hipEventCreate");
+        }
+    }
+    for (uint32_t i = 0; i < warmup && !rc; ++i) rc = gemm_locked(dev, d);
+    for (uint32_t i = 0; i <= iters && !rc; ++i) {
+        hipError_t he = T0G_HIP(hipEventRecord(ev[i], dev->stream));
+        if (he != hipSuccess) rc = poison(dev, hip_fail(he, "hipEventRecord"));
+        else if (i < iters) rc = gemm_locked(dev, d);
+    }
+    if (!rc) rc = wait_stream(dev);
+    if (!rc) {
+        ms->assign(iters, 0.0);
+        for (uint32_t i = 0; i < iters && !rc; ++i) {
+            float t = 0.f;
+            hipError_t he = T0G_HIP(hipEventElapsedTime(&t, ev[i], ev[i + 1]));
+            if (he != hipSuccess) rc = hip_fail(he, "hipEventElapsedTime");
+            (*ms)[i] = t;
+        }
+    }
+    destroy();
+    return rc;
+}
+
+}  // namespace t0g
+
+extern "C" {
+
 // ---- Ignis bf16_matmul caller path ------------------------------------------
 
 static int convert_locked(t0g_device *dev, uint64_t src, uint64_t dst, uint64_t n) {

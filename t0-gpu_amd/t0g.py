@@ -205,6 +205,44 @@ _sig("t0g_matmul_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_backward_data_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_backward_weight_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_wt_bf16_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
+
+
+class TuneResult(ctypes.Structure):
+    """GemmTuneResult (src/t0/auto_gemm.rs:28-42) without the ranking (GemmTuner.ranking)."""
+
+    _fields_ = [
+        ("best", GemmConfig),
+        ("best_tflops", ctypes.c_double),
+        ("m", ctypes.c_uint32),
+        ("n", ctypes.c_uint32),
+        ("k", ctypes.c_uint32),
+        ("transpose", ctypes.c_uint32),
+        ("out_dtype", ctypes.c_uint32),
+        ("from_cache", ctypes.c_int32),
+        ("n_all", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+_tunerp = ctypes.POINTER(_p)
+_sig("t0g_tuner_create", ctypes.c_int, ctypes.c_char_p, _tunerp)
+_sig("t0g_tuner_destroy", ctypes.c_int, _p)
+_sig("t0g_tuner_global", ctypes.c_int, _tunerp)
+_sig("t0g_tuner_set_params", ctypes.c_int, _p, _u32, _u32)
+_sig("t0g_tuner_get_params", ctypes.c_int, _p, _u32p, _u32p, _u32p)
+_sig("t0g_tuner_cache_dir", ctypes.c_int, _p, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_tune_candidates", ctypes.c_int, _u32, _u32, _u32, _u32, _u32, _cfgp, _u32p)
+_sig("t0g_tuner_tune", ctypes.c_int, _p, _p, _u32, _u32, _u32, _u32, _u32, _cfgp)
+_sig("t0g_tuner_lookup", ctypes.c_int, _p, _u32, _u32, _u32, _u32, _u32, ctypes.POINTER(TuneResult),
+     ctypes.POINTER(ctypes.c_int))
+_sig("t0g_tuner_ranking", ctypes.c_int, _p, _u32, _u32, _u32, _u32, _u32, _u32, ctypes.c_char_p, ctypes.c_size_t,
+     ctypes.POINTER(ctypes.c_double))
+_sig("t0g_tuner_store", ctypes.c_int, _p, ctypes.POINTER(TuneResult), ctypes.POINTER(ctypes.c_char_p),
+     ctypes.POINTER(ctypes.c_double), _u32)
+_sig("t0g_tuner_invalidate", ctypes.c_int, _p, _u32, _u32, _u32, _u32, _u32)
+_sig("t0g_tuner_clear", ctypes.c_int, _p)
+_sig("t0g_tuner_report", ctypes.c_int, _p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t))
+_sig("t0g_auto_gemm", ctypes.c_int, _p, _p, _u64, _u64, _u64, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_double))
 _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 
@@ -536,3 +574,147 @@ class GpuRuntime:
     def matmul_wt_bf16_f32(self, x, wt_bf16, y, m, k, n):
         """matmul_with_wt_bf16: Y[M,N] = bf16(X[M,K]) WT[N,K]^T."""
         _check(_lib.t0g_matmul_wt_bf16_f32(self.handle, x, wt_bf16, y, m, k, n))
+
+
+# ---- autotuner (src/t0/auto_gemm.rs) -----------------------------------------
+
+def _layout(t):
+    return LAYOUTS[t.upper()] if isinstance(t, str) else int(t)
+
+
+def tune_candidates(m, n, k, transpose=NT, max_count=64):
+    """The configs GemmTuner.tune benchmarks, best modelled first."""
+    arr = (GemmConfig * max_count)()
+    cnt = ctypes.c_uint32()
+    _check(_lib.t0g_tune_candidates(m, n, k, _layout(transpose), max_count, arr, ctypes.byref(cnt)))
+    return [arr[i].copy() for i in range(cnt.value)]
+
+
+class GemmTuner:
+    """GemmTuner (src/t0/auto_gemm.rs:46-417): GPU-benchmarked config choice with
+    an in-memory and on-disk cache (one JSON file per problem)."""
+
+    def __init__(self, handle, owned=True):
+        self.handle = handle
+        self._owned = owned
+
+    @staticmethod
+    def new():
+        h = _p()
+        _check(_lib.t0g_tuner_create(None, ctypes.byref(h)))
+        return GemmTuner(h)
+
+    @staticmethod
+    def with_cache_dir(path):
+        h = _p()
+        _check(_lib.t0g_tuner_create(os.fsencode(str(path)), ctypes.byref(h)))
+        return GemmTuner(h)
+
+    @staticmethod
+    def global_tuner():
+        h = _p()
+        _check(_lib.t0g_tuner_global(ctypes.byref(h)))
+        return GemmTuner(h, owned=False)
+
+    def close(self):
+        if self.handle and self._owned:
+            _check(_lib.t0g_tuner_destroy(self.handle))
+        self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _params(self):
+        mc, it, nc = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        _check(_lib.t0g_tuner_get_params(self.handle, ctypes.byref(mc), ctypes.byref(it), ctypes.byref(nc)))
+        return mc.value, it.value, nc.value
+
+    @property
+    def max_candidates(self):
+        return self._params()[0]
+
+    @max_candidates.setter
+    def max_candidates(self, v):
+        _check(_lib.t0g_tuner_set_params(self.handle, v, self.n_iters))
+
+    @property
+    def n_iters(self):
+        return self._params()[1]
+
+    @n_iters.setter
+    def n_iters(self, v):
+        _check(_lib.t0g_tuner_set_params(self.handle, self.max_candidates, v))
+
+    def __len__(self):
+        return self._params()[2]
+
+    @property
+    def cache_dir(self):
+        buf = ctypes.create_string_buffer(4096)
+        _check(_lib.t0g_tuner_cache_dir(self.handle, buf, len(buf)))
+        return buf.value.decode()
+
+    def tune(self, rt, m, n, k, transpose=NT, out_dtype=F32):
+        """GemmTuner::tune(rt, m, n, k) -> best GemmConfig (argument order as the reference)."""
+        cfg = GemmConfig()
+        _check(_lib.t0g_tuner_tune(self.handle, rt.handle, m, n, k, _layout(transpose), out_dtype,
+                                   ctypes.byref(cfg)))
+        return cfg
+
+    def lookup(self, m, n, k, transpose=NT, out_dtype=F32):
+        """The cached TuneResult (memory, then disk) or None."""
+        r = TuneResult()
+        found = ctypes.c_int()
+        _check(_lib.t0g_tuner_lookup(self.handle, m, n, k, _layout(transpose), out_dtype, ctypes.byref(r),
+                                     ctypes.byref(found)))
+        return r if found.value else None
+
+    def ranking(self, m, n, k, transpose=NT, out_dtype=F32):
+        """GemmTuneResult::all: [(config name, TFLOPS)], fastest first."""
+        r = self.lookup(m, n, k, transpose, out_dtype)
+        if r is None:
+            return []
+        out = []
+        buf = ctypes.create_string_buffer(256)
+        tf = ctypes.c_double()
+        for i in range(r.n_all):
+            _check(_lib.t0g_tuner_ranking(self.handle, m, n, k, _layout(transpose), out_dtype, i, buf, len(buf),
+                                          ctypes.byref(tf)))
+            out.append((buf.value.decode(), tf.value))
+        return out
+
+    def save_cache(self, m, n, k, best, best_tflops, all_=(), transpose=NT, out_dtype=F32):
+        """save_cache (src/t0/auto_gemm.rs:364-391) of a result and its ranking."""
+        r = TuneResult()
+        r.best = best
+        r.best_tflops = best_tflops
+        r.m, r.n, r.k = m, n, k
+        r.transpose = _layout(transpose)
+        r.out_dtype = out_dtype
+        names = (ctypes.c_char_p * max(1, len(all_)))(*[nm.encode() for nm, _ in all_])
+        tfs = (ctypes.c_double * max(1, len(all_)))(*[t for _, t in all_])
+        _check(_lib.t0g_tuner_store(self.handle, ctypes.byref(r), names, tfs, len(all_)))
+
+    def invalidate(self, m, n, k, transpose=NT, out_dtype=F32):
+        _check(_lib.t0g_tuner_invalidate(self.handle, m, n, k, _layout(transpose), out_dtype))
+
+    def clear(self):
+        _check(_lib.t0g_tuner_clear(self.handle))
+
+    def report(self):
+        need = ctypes.c_size_t()
+        _check(_lib.t0g_tuner_report(self.handle, None, 0, ctypes.byref(need)))
+        buf = ctypes.create_string_buffer(need.value)
+        _check(_lib.t0g_tuner_report(self.handle, buf, len(buf), ctypes.byref(need)))
+        return buf.value.decode()
+
+
+def auto_gemm(rt, a, b, c, m, n, k, tuner=None):
+    """auto_gemm(rt, a, b, c, m, n, k) (src/t0/auto_gemm.rs:445-480): tune (NT, f32 out)
+    and run C = A * B^T with the best config, synchronously; returns the cached TFLOPS."""
+    tf = ctypes.c_double()
+    _check(_lib.t0g_auto_gemm(tuner.handle if tuner is not None else None, rt.handle, a, b, c, m, n, k, ctypes.byref(tf)))
+    return tf.value
