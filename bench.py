@@ -194,6 +194,27 @@ def tuner_extra(t0g, torch, rt, stream, steps, warmup):
     return out
 
 
+def stream_k_extra(t0g, torch, rt, stream, steps, warmup):
+    """The stream-K schedule against the data-parallel / split-K ones: a tile count
+    just past 256 (272 tiles, where auto_select takes stream-K) and the MLP forward
+    shape (172 tiles, where it does not)."""
+    p256 = t0g.GemmConfig.preset("tile_256x256_k64")
+    sk = p256.copy(split_k=t0g.STREAM_K)
+    out = {}
+    for lay, m, n, k, others in [("NN", 4352, 4096, 8192, {"dp": p256, "split2": p256.copy(split_k=2)}),
+                                 ("NN", 1024, 11008, 4096, {"dp": p256})]:
+        line = {"auto_select": t0g.auto_select(m, k, n).name()}
+        r = time_gemm(t0g, torch, rt, stream, m, n, k, lay, steps, warmup, seed=17, config=sk)
+        line["stream_k_us"] = round(r["event_ms_per_launch"] * 1e3, 2)
+        line["stream_k_tflops"] = round(r["flop"] / (r["event_ms_per_launch"] * 1e-3) / 1e12, 1)
+        for name, cfg in others.items():
+            r = time_gemm(t0g, torch, rt, stream, m, n, k, lay, steps, warmup, seed=17, config=cfg)
+            line[f"{name}_us"] = round(r["event_ms_per_launch"] * 1e3, 2)
+        out[f"{lay.lower()}_{m}x{n}x{k}"] = line
+    out["ready_flag_timeouts"] = rt.stream_k_timeouts()
+    return out
+
+
 def cpu_baseline(torch, tensors, m, n, k, min_seconds):
     """The CPU oracle (oracle/ref_gemm.c, a bit-exact restatement of the reference's
     CPU GEMM) on this host: the whole 4096^3 product, repeated to ~min_seconds."""
@@ -350,6 +371,8 @@ def main():
                                                      max(2, args.warmup // 10))
         log("[bench] GemmTuner on the BASELINE shapes")
         extra["tuner"] = tuner_extra(t0g, torch, rt, stream, max(10, args.steps // 2), max(10, args.warmup // 4))
+        log("[bench] stream-K")
+        extra["stream_k"] = stream_k_extra(t0g, torch, rt, stream, max(10, args.steps // 4), max(10, args.warmup // 8))
         log("[bench] Ignis f32 caller path")
         extra["ignis"] = ignis_linear(torch, rt, stream, max(5, args.steps // 2), max(3, args.warmup // 4))
         line["extra"] = extra

@@ -78,7 +78,8 @@ typedef enum t0g_epilogue_op {
 typedef enum t0g_dtype { T0G_F32 = 0, T0G_BF16 = 1 } t0g_dtype;
 
 /* GemmConfig (src/t0/gemm_gen.rs:56-84).  Same fields and meaning; the valid
- * tile set is the MI355X one (t0g_config_preset).  split_k: 0 = None. */
+ * tile set is the MI355X one (t0g_config_preset).  split_k: 0 = None, or
+ * T0G_STREAM_K. */
 typedef struct t0g_gemm_config {
     uint32_t tile_m;
     uint32_t tile_n;
@@ -94,6 +95,15 @@ typedef struct t0g_gemm_config {
     uint32_t transpose;     /* t0g_transpose */
     uint32_t epilogue;      /* t0g_epilogue */
 } t0g_gemm_config;
+
+/* split_k value selecting the stream-K schedule (no reference counterpart; the
+ * reference evaluated and rejected stream-K on gfx1100): one workgroup per CU,
+ * each taking an equal share of all (tile, 64-wide K step) pairs; tiles cut
+ * between workgroups are summed in a fixed order, so results are deterministic.
+ * 256x256 tile only; runs through t0g_gemm (not the reference-layout
+ * t0g_kernel_get / t0g_dispatch path); operands that do not meet the fast
+ * path's alignment fall back to the data-parallel 128x128 kernel. */
+#define T0G_STREAM_K 0x80000000u
 
 typedef struct t0g_device t0g_device;
 typedef struct t0g_kernel t0g_kernel;
@@ -369,6 +379,14 @@ T0G_API int t0g_auto_gemm(t0g_tuner *tuner, t0g_device *dev, uint64_t a, uint64_
                           uint32_t n, uint32_t k, double *tflops);
 
 /* ---- test hooks ------------------------------------------------------------ */
+/* The stream-K partition (one range of (tile, K step) pairs per workgroup):
+ * first pair of logical workgroup w (w = grid gives total), and the workgroup
+ * whose range holds pair `it`.  Host only. */
+T0G_API uint32_t t0g_stream_k_begin(uint32_t total, uint32_t grid, uint32_t w);
+T0G_API uint32_t t0g_stream_k_worker(uint32_t total, uint32_t grid, uint32_t it);
+/* Ready-flag waits of stream-K launches on dev that gave up (0 unless a
+ * workgroup waited past its spin limit); waits for the device stream. */
+T0G_API int t0g_stream_k_timeouts(t0g_device *dev, uint32_t *count);
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
  * real device fault. */

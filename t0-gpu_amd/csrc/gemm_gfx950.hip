@@ -1166,6 +1166,20 @@ extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvert
     T0G_GEMM_256(t0g_gemm_256x256_k64_tt_##OUTN, false, true, OBF)
 T0G_GEMM_LAYOUTS_256(f32, false)
 T0G_GEMM_LAYOUTS_256(bf16, true)
+
+// The same tiles on a stream-K schedule (suffix _sk, T0gGemmSkArgs).
+#define T0G_GEMM_256_SK(NAME, AK, BKM, OBF)                                                               \
+    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
+        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmSkArgs s) {              \
+        t0g::gemm_tile_sk<AK, BKM, OBF>(s);                                                              \
+    }
+#define T0G_GEMM_LAYOUTS_256_SK(OUTN, OBF)                                   \
+    T0G_GEMM_256_SK(t0g_gemm_256x256_k64_nt_##OUTN##_sk, true, true, OBF)    \
+    T0G_GEMM_256_SK(t0g_gemm_256x256_k64_nn_##OUTN##_sk, true, false, OBF)   \
+    T0G_GEMM_256_SK(t0g_gemm_256x256_k64_tn_##OUTN##_sk, false, false, OBF)  \
+    T0G_GEMM_256_SK(t0g_gemm_256x256_k64_tt_##OUTN##_sk, false, true, OBF)
+T0G_GEMM_LAYOUTS_256_SK(f32, false)
+T0G_GEMM_LAYOUTS_256_SK(bf16, true)
 T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)

@@ -326,9 +326,21 @@ struct VecEpilogue16 {
     static constexpr uint32_t kWaveBytes = 32 * kStride;
 };
 
-template <int SM, int SN, bool OUT_BF16>
+// Partial tiles that other workgroups left for this one (stream-K): `count`
+// slots from `first`, summed in slot order onto the workgroup's own
+// accumulators.  A slot holds a whole 256 x 256 f32 tile in accumulator order:
+// sub-tile (i, j) of wave v is 1 KB at ((v * SM + i) * SN + j) KB, 16 bytes per
+// lane; `frag` is this lane's offset of sub-tile (0, 0).
+struct SkFixup {
+    uint64_t base;
+    uint32_t first, count;
+    uint32_t frag;
+};
+
+template <int SM, int SN, bool OUT_BF16, bool FIXUP = false>
 __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32x4_t (&acc)[SM][SN], uint32_t row0,
-                                                 uint32_t col0, uint32_t lane, uint32_t lds, bool vec) {
+                                                 uint32_t col0, uint32_t lane, uint32_t lds, bool vec,
+                                                 SkFixup fx = SkFixup{0, 0, 0, 0}) {
     typedef VecEpilogue16<SN> E;
     typedef __attribute__((address_space(3))) float lds_f32;
     typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
@@ -354,6 +366,29 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
     const uint32_t esize = OUT_BF16 ? 2u : 4u;
 #pragma unroll
     for (int i2 = 0; i2 < SM; i2 += 2) {
+        f32x4_t x[2][SN];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) x[ii][j] = acc[i2 + ii][j];
+        if constexpr (FIXUP) {
+            // all of a slot's loads for this block are issued before any is used
+            for (uint32_t s = 0; s < fx.count; ++s) {
+                const uint64_t sb =
+                    fx.base + (uint64_t)(fx.first + s) * T0G_SK_SLOT_BYTES + fx.frag + (uint32_t)(i2 * SN) * 1024u;
+                f32x4_t t[2][SN];
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < SN; ++j)
+                        t[ii][j] = *reinterpret_cast<const volatile __attribute__((address_space(1))) f32x4_t*>(
+                            (uintptr_t)(sb + (uint32_t)(ii * SN + j) * 1024u));
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < SN; ++j) x[ii][j] += t[ii][j];
+            }
+        }
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -362,7 +397,7 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = 16 * ii + 4 * q + r;
                     *reinterpret_cast<lds_f32*>((uintptr_t)(lds + row * E::kStride + (j * 16 + l16) * 4)) =
-                        acc[i2 + ii][j][r];
+                        x[ii][j][r];
                 }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -412,6 +447,18 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
 
 // Output tile of this workgroup: block ids remapped so each XCD (own L2) works
 // on a contiguous patch, walked in groups of group_m tile rows.
+template <int BM, int BN>
+__device__ __forceinline__ void tile_of_index(const T0gGemmArgs& p, uint32_t bid, uint32_t& m0, uint32_t& n0) {
+    const uint32_t gm = p.group_m;
+    const uint32_t per_group = gm * p.tiles_n;
+    const uint32_t group = bid / per_group;
+    const uint32_t first_m = group * gm;
+    const uint32_t gsz = min(p.tiles_m - first_m, gm);
+    const uint32_t in_group = bid - group * per_group;
+    m0 = (first_m + in_group % gsz) * BM;
+    n0 = (in_group / gsz) * BN;
+}
+
 template <int BM, int BN>
 __device__ __forceinline__ void tile_origin(const T0gGemmArgs& p, uint32_t& m0, uint32_t& n0) {
     uint32_t bid = blockIdx.x;
@@ -607,6 +654,237 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
     const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
     store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
                                        lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+}
+
+// ---- stream-K ------------------------------------------------------------------
+// The 256x256 kernels above on a stream-K schedule (T0gGemmSkArgs): `grid`
+// workgroups, one per CU, each take an equal contiguous range of the GEMM's
+// (tile, 64-wide K iteration) pairs, tiles in index order and K ascending
+// within a tile.  A workgroup walks the tiles of its range from the last to the
+// first.  The last tile of its range is usually cut (its K tail belongs to the
+// next workgroups): the workgroup writes that partial tile to its slot, makes
+// it visible at device scope and raises its ready flag; it does this first, so
+// the partial is ready early.  Every other tile of its range it owns (its range
+// holds the tile's last K iteration): it computes its part, waits for the ready
+// flags of the lower workgroups that hold the rest of the tile (those wrote
+// the partial at the start of their own work), adds their partials in slot
+// order and runs the epilogue.
+//
+// Waits only go to lower logical ids, and logical ids are tickets drawn from a
+// device counter as each workgroup starts, so every workgroup waited for has
+// already started and never waits for a later one: no deadlock, whether or not
+// the whole grid is resident.  A wait gives up after spin_limit polls (and
+// counts a timeout) so that every workgroup ends.  The last workgroup to finish
+// resets the ticket and done counters; owners clear the flags they consumed:
+// the control block is all zero again for the next launch.
+// Partial tiles and ready flags cross XCDs, whose L2 caches are not coherent
+// with each other for this memory.  Instead of fences (a release writes back,
+// an acquire invalidates, the whole L2 of the XCD, which costs every other
+// workgroup there its cached operand panels), partials are written and read
+// with volatile accesses, which bypass the caches, and flags with relaxed
+// device-scope atomics; vmcnt(0) and a barrier order the partial's stores
+// before the flag.
+typedef volatile __attribute__((address_space(1))) f32x4_t gvf32x4_t;
+
+template <int SM, int SN>
+__device__ __forceinline__ void store_partial16(const f32x4_t (&acc)[SM][SN], uint64_t slot_frag) {
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+            *reinterpret_cast<gvf32x4_t*>((uintptr_t)(slot_frag + (uint32_t)(i * SN + j) * 1024u)) = acc[i][j];
+}
+
+// Loop state lives in LDS and is read back after the K loop: the pipeline
+// needs nearly all SGPRs, and values kept live across it would be spilled.
+struct SkRange {
+    uint32_t w, t;   // logical workgroup id, current tile
+};
+
+// threadIdx.x through an opaque move: values derived from it in one phase of
+// the tile loop cannot be hoisted out of the loop and kept live (in VGPRs)
+// across the other phase's K loop.
+__device__ __forceinline__ uint32_t opaque_tid() {
+    uint32_t t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((uint32_t)threadIdx.x));
+    return t;
+}
+
+// A fresh, wave-uniform copy of a kernel-argument block kept in LDS: the
+// kernarg values themselves would otherwise be held in SGPRs for the whole
+// tile loop.  The asm barrier makes every phase read LDS again.
+template <class T>
+__device__ __forceinline__ T lds_args(const T& src) {
+    static_assert(sizeof(T) % 16 == 0, "whole 16-byte words");
+    asm volatile("" ::: "memory");
+    typedef const __attribute__((address_space(3))) u32x4_t lds_u32x4;
+    const uint32_t base = lds_addr(reinterpret_cast<const char*>(&src));
+    uint32_t w[sizeof(T) / 4];
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(T) / 16; ++i) {
+        const u32x4_t v = *reinterpret_cast<lds_u32x4*>((uintptr_t)(base + 16 * i));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[4 * i + c] = (uint32_t)__builtin_amdgcn_readfirstlane(v[c]);
+    }
+    return __builtin_bit_cast(T, w);
+}
+
+__device__ __forceinline__ SkRange sk_state(const SkRange* st) {
+    const volatile SkRange* v = st;
+    return SkRange{(uint32_t)__builtin_amdgcn_readfirstlane(v->w), (uint32_t)__builtin_amdgcn_readfirstlane(v->t)};
+}
+
+template <bool A_K, bool B_K, bool OUT_BF16>
+__device__ __forceinline__ void gemm_tile_sk(const T0gGemmSkArgs& kargs) {
+    constexpr bool PP = A_K;   // same kernel choice per layout as the data-parallel 256x256 kernels
+    constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = PP ? 4 : 2;
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int SM = WTM / 16, SN = WTN / 16;
+    using OpA = Op16<A_K, BM, NT, SM>;
+    using OpB = Op16<B_K, BN, NT, SN>;
+    constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
+    constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
+    static_assert((NT / 64) * SM * SN * 1024 == T0G_SK_SLOT_BYTES, "a partial tile fills one slot");
+    static_assert((NT / 64) * VecEpilogue16<SN>::kWaveBytes <= 2 * STAGE, "epilogue staging must fit the stages");
+    typedef __attribute__((address_space(1))) uint32_t gu32_t;
+    static_assert(sizeof(T0gGemmSkArgs) % 16 == 0, "argument block copied in 16-byte words");
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    __shared__ SkRange s_state;
+    __shared__ __attribute__((aligned(16))) T0gGemmSkArgs s_args;
+
+    if (threadIdx.x == 0) {
+        s_args = kargs;
+        gu32_t* const ctl = reinterpret_cast<gu32_t*>((uintptr_t)kargs.sync);
+        const uint32_t w = __hip_atomic_fetch_add(ctl + T0G_SK_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t total = kargs.g.tiles_m * kargs.g.tiles_n * kargs.iters_per_tile;
+        const uint32_t it0 = t0g_sk_begin(total, kargs.grid, w), it1 = t0g_sk_begin(total, kargs.grid, w + 1);
+        s_state.w = w;
+        s_state.t = it1 > it0 ? (it1 - 1) / kargs.iters_per_tile : 0xFFFFFFFFu;   // all ones: empty range
+        if (w >= kargs.grid) {
+            // control block not at zero (a launch overlapping this one): do nothing
+            // rather than touch slots and flags past the grid
+            s_state.t = 0xFFFFFFFFu;
+            __hip_atomic_fetch_add(ctl + T0G_SK_TIMEOUTS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+
+    for (;;) {
+        f32x4_t acc[SM][SN];
+        {
+            const T0gGemmSkArgs s = lds_args(s_args);
+            const T0gGemmArgs& p = s.g;
+            const uint32_t tid = opaque_tid();
+            const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+            const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+            const SkRange st = sk_state(&s_state);
+            if (st.t == 0xFFFFFFFFu) break;
+            const uint32_t ipt = s.iters_per_tile, total = p.tiles_m * p.tiles_n * ipt;
+            const uint32_t tb = st.t * ipt;
+            const uint32_t it0 = t0g_sk_begin(total, s.grid, st.w), it1 = t0g_sk_begin(total, s.grid, st.w + 1);
+            const uint32_t kb = it0 > tb ? it0 - tb : 0u, ke = it1 < tb + ipt ? it1 - tb : ipt;
+            uint32_t m0, n0;
+            tile_of_index<BM, BN>(p, st.t, m0, n0);
+            const uint32_t kbeg = kb * 64u, kend = min(p.k, ke * 64u);
+            const int nst = (int)(ke - kb);
+            const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+            const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+            const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+            OpA la;
+            OpB lb;
+            la.init(tid, m0, p.lda, wm * WTM);
+            lb.init(tid, n0, p.ldb, wn * WTN);
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j) acc[i][j] = f32x4_t{};
+            mfma16_drain();
+            if constexpr (PP) {
+                const uint32_t group = wave >> 2;
+                if ((kend - kbeg) % 64 == 0)
+                    k_pipeline_pp<false, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0,
+                                                         group);
+                else
+                    k_pipeline_pp<true, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0,
+                                                        group);
+            } else {
+                if ((kend - kbeg) % 64 == 0)
+                    k_pipeline16<false, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
+                                                                       nst, lds0);
+                else
+                    k_pipeline16<true, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
+                                                                      nst, lds0);
+            }
+            mfma16_drain();
+            T0G_WAIT_VMCNT(0);
+            barrier_no_fence();
+        }
+
+        // after the K loop: everything is recomputed from the LDS state
+        const T0gGemmSkArgs s = lds_args(s_args);
+        const T0gGemmArgs& p = s.g;
+        gu32_t* const ctl = reinterpret_cast<gu32_t*>((uintptr_t)s.sync);
+        const uint32_t tid = opaque_tid();
+        const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+        const SkRange st = sk_state(&s_state);
+        const uint32_t ipt = s.iters_per_tile, total = p.tiles_m * p.tiles_n * ipt;
+        const uint32_t tb = st.t * ipt;
+        const uint32_t it0 = t0g_sk_begin(total, s.grid, st.w), it1 = t0g_sk_begin(total, s.grid, st.w + 1);
+        const uint32_t frag = wave * (uint32_t)(SM * SN) * 1024u + lane * 16u;
+        gu32_t* const ready = ctl + T0G_SK_CTL_WORDS;
+        if (it1 < tb + ipt) {
+            // the tile's K tail belongs to later workgroups: leave the partial
+            store_partial16<SM, SN>(acc, s.partials + (uint64_t)st.w * T0G_SK_SLOT_BYTES + frag);
+            T0G_WAIT_VMCNT(0);
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(ready + st.w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            const uint32_t first = tb < it0 ? t0g_sk_worker(total, s.grid, tb) : st.w;
+            if (first < st.w) {
+                if (tid == 0) {
+                    for (uint32_t j = first; j < st.w; ++j) {
+                        for (uint32_t n = 0;
+                             __hip_atomic_load(ready + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++n) {
+                            if (n >= s.spin_limit) {
+                                __hip_atomic_fetch_add(ctl + T0G_SK_TIMEOUTS, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+                                break;
+                            }
+                            __builtin_amdgcn_s_sleep(2);
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+            uint32_t m0, n0;
+            tile_of_index<BM, BN>(p, st.t, m0, n0);
+            const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+            store_tile_vec16<SM, SN, OUT_BF16, true>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                                     lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec,
+                                                     SkFixup{s.partials, first, st.w - first, frag});
+            if (first < st.w) {
+                __syncthreads();
+                if (tid == 0)
+                    for (uint32_t j = first; j < st.w; ++j)
+                        __hip_atomic_store(ready + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        // next tile down, or done; the barrier also ends the epilogue's use of LDS
+        // before the next K loop's DMA
+        __syncthreads();
+        if (tid == 0) s_state.t = tb > it0 ? st.t - 1 : 0xFFFFFFFFu;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        gu32_t* const ctl = reinterpret_cast<gu32_t*>((uintptr_t)kargs.sync);
+        const uint32_t done = __hip_atomic_fetch_add(ctl + T0G_SK_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == kargs.grid - 1) {
+            __hip_atomic_store(ctl + T0G_SK_TICKET, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ctl + T0G_SK_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 }  // namespace t0g

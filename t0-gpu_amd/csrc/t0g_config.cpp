@@ -10,6 +10,7 @@
 
 #include "t0g.h"
 #include "t0g_internal.h"
+#include "t0g_kernel_args.h"
 
 namespace t0g {
 
@@ -82,6 +83,12 @@ int validate(const t0g_gemm_config *cfg) {
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "n_col_passes must be 1 on gfx950 (got %u)", cfg->n_col_passes);
     if (cfg->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", cfg->transpose);
     if (cfg->epilogue > T0G_EPI_BIAS_ADD_RELU) return fail(T0G_ERR_INVALID_ARG, "bad epilogue %u", cfg->epilogue);
+    if (cfg->split_k == T0G_STREAM_K) {
+        if (cfg->tile_m != 256 || cfg->tile_n != 256)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the 256x256 tile (got %ux%u)", cfg->tile_m,
+                        cfg->tile_n);
+        return ok();
+    }
     const uint32_t sk = cfg_split(cfg);
     if (sk > kMaxSplitK || (sk & (sk - 1)) != 0)
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u must be a power of two <= %u", sk, kMaxSplitK);
@@ -114,6 +121,21 @@ double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint3
     return t_us;
 }
 
+// Stream-K on the 256x256 tile: every CU runs ceil(pairs / 256) K steps at
+// the one-workgroup rate, plus the per-tile fixed cost and, when tiles are cut
+// between workgroups, ~30 us for partial tiles and the extra tile prologues and
+// epilogues (measured 22-44 us on MI355X over tile counts of 172-400).
+double model_time_sk_us(uint32_t m, uint32_t k, uint32_t n) {
+    const TileDef &t = kTiles[0];
+    const uint64_t tiles = (uint64_t)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const uint64_t ipt = (k + kTileK - 1) / kTileK;
+    const uint64_t total = tiles * ipt;
+    if (total == 0) return 1e300;
+    const uint64_t per_cu = (total + kNumCUs - 1) / kNumCUs;
+    const bool cut = total % kNumCUs != 0 || per_cu % ipt != 0;
+    return t.t0_us + (double)per_cu * 2.0 * t.bm * t.bn * kTileK / t.rate1 * 1e-3 + (cut ? 30.0 : 5.0);
+}
+
 void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
     const TileDef *best = &kTiles[0];
     uint32_t best_sk = 1;
@@ -128,6 +150,20 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
                 best_sk = sk;
             }
         }
+    }
+    // Stream-K only where data-parallel rounds quantise badly: a last round at
+    // most an eighth full after at least one full one, and a clear modelled
+    // margin.  A part-empty round costs far less than its share of CUs
+    // suggests (the busy CUs clock up under the board power limit), so
+    // stream-K measured slower or equal at 144, 172 and 576 tiles and faster at
+    // 272 (4352x4096x8192: 267 us against 316 us); the tuner measures the rest.
+    const TileDef &big = kTiles[0];
+    const uint64_t tiles256 = (uint64_t)((m + big.bm - 1) / big.bm) * ((n + big.bn - 1) / big.bn);
+    const uint64_t last_round = tiles256 % kNumCUs;
+    if (tiles256 > kNumCUs && last_round != 0 && last_round * 8 <= kNumCUs &&
+        model_time_sk_us(m, k, n) < 0.85 * best_t) {
+        best = &kTiles[0];
+        best_sk = T0G_STREAM_K;
     }
     make_config(*best, best_sk, out);
 }
@@ -201,7 +237,8 @@ int t0g_config_name(const t0g_gemm_config *cfg, char *buf, size_t len) {
     std::string s = "t0_gemm_" + std::to_string(cfg->tile_m) + "x" + std::to_string(cfg->tile_n) + "_k" +
                     std::to_string(cfg->tile_k);
     s += cfg->use_lds ? (cfg->double_buffer ? "_ldsdb" : "_lds") : "_direct";
-    if (cfg->split_k > 1) s += "_sk" + std::to_string(cfg->split_k);
+    if (cfg->split_k == T0G_STREAM_K) s += "_streamk";
+    else if (cfg->split_k > 1) s += "_sk" + std::to_string(cfg->split_k);
     if (cfg->n_col_passes > 1) s += "_" + std::to_string(cfg->n_col_passes) + "p";
     if (!cfg->swap_grid) s += "_mg";
     if (cfg->wgp_mode) s += "_wgp";
@@ -228,8 +265,17 @@ int t0g_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose,
     return rc;
 }
 
+// The stream-K schedule has its own launch shape and argument block: it runs
+// through t0g_gemm only, not through the reference's grid/kernarg/dispatch path.
+static int no_stream_k(const t0g_gemm_config *cfg) {
+    if (cfg->split_k == T0G_STREAM_K)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K configs run through t0g_gemm only");
+    return T0G_OK;
+}
+
 static int grid_common(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t sk, uint32_t *gx, uint32_t *gy) {
     if (!cfg || !gx || !gy) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = no_stream_k(cfg)) return rc;
     if (cfg->tile_m == 0 || cfg->tile_n == 0) return fail(T0G_ERR_INVALID_ARG, "zero tile size");
     const uint32_t eff_n = cfg->tile_n * (cfg->n_col_passes ? cfg->n_col_passes : 1);
     const uint32_t tm = (m + cfg->tile_m - 1) / cfg->tile_m;
@@ -257,6 +303,7 @@ int t0g_compute_grid_split_k(const t0g_gemm_config *cfg, uint32_t m, uint32_t n,
 
 int t0g_compute_grid_auto(const t0g_gemm_config *cfg, uint32_t m, uint32_t n, uint32_t *gx, uint32_t *gy) {
     if (!cfg) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = no_stream_k(cfg)) return rc;
     const uint32_t sk = cfg_split(cfg);
     return sk > 1 ? t0g_compute_grid_split_k(cfg, m, n, sk, gx, gy) : t0g_compute_grid(cfg, m, n, gx, gy);
 }
@@ -274,6 +321,7 @@ static void put_u32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
 int t0g_build_kernargs(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
                        const t0g_gemm_config *cfg, uint8_t out[40]) {
     if (!cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = no_stream_k(cfg)) return rc;
     const uint32_t sk = cfg_split(cfg);
     const uint32_t y_stride = sk > 1 ? m * n * 4 : 0;
     put_u64(out + 0, x);
@@ -296,6 +344,7 @@ int t0g_build_kernargs_with_bias(uint64_t x, uint64_t wt, uint64_t y, uint32_t k
 int t0g_build_kernargs_m(uint64_t x, uint64_t wt, uint64_t y, uint32_t k, uint32_t n, uint32_t m,
                          const t0g_gemm_config *cfg, uint8_t out[44]) {
     if (!cfg || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = no_stream_k(cfg)) return rc;
     uint32_t shift = 0;
     switch (cfg_split(cfg)) {
         case 2: shift = 1; break;
@@ -363,6 +412,14 @@ int t0g_build_kernargs_m_epilogue(uint64_t x, uint64_t wt, uint64_t y, uint32_t 
     }
     *len = off;
     return ok();
+}
+
+uint32_t t0g_stream_k_begin(uint32_t total, uint32_t grid, uint32_t w) {
+    return grid ? t0g_sk_begin(total, grid, w) : 0;
+}
+
+uint32_t t0g_stream_k_worker(uint32_t total, uint32_t grid, uint32_t it) {
+    return grid && total >= grid ? t0g_sk_worker(total, grid, it) : 0;
 }
 
 int t0g_auto_select_backward_data(uint32_t m, uint32_t n_orig, uint32_t k_orig, t0g_gemm_config *out) {

@@ -41,6 +41,7 @@ uint32_t cfg_split(const t0g_gemm_config *cfg);
 int validate(const t0g_gemm_config *cfg);
 void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
 double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);
+double model_time_sk_us(uint32_t m, uint32_t k, uint32_t n);   // stream-K, 256x256 tile
 
 // Epilogue chains (t0g_epilogue_op codes, 4 bits each, first op lowest).
 constexpr uint32_t kMaxChainOps = 8;

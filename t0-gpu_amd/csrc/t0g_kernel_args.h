@@ -28,6 +28,47 @@ typedef struct T0gGemmArgs {
     uint32_t reserved;
 } T0gGemmArgs;
 
+/* Stream-K launch of the 256x256 tile: the GEMM's tiles x iterations_per_tile
+ * K iterations (64 K values each) are dealt out in equal contiguous ranges to
+ * `grid` workgroups; a tile cut between workgroups is finished by the one that
+ * holds its last iteration (the owner), after it has added the fp32 partial
+ * tiles the others left in their slots. */
+typedef struct T0gGemmSkArgs {
+    T0gGemmArgs g;           /* problem, operands, epilogue; k_per_split = k    */
+    uint64_t partials;       /* f32 [grid][256 * 256]: one partial tile per workgroup */
+    uint64_t sync;           /* u32: 16 control words (ticket, done, timeouts), then
+                                one ready flag per workgroup; all zero between launches */
+    uint32_t grid;           /* launched workgroups, <= tiles * iters_per_tile    */
+    uint32_t iters_per_tile; /* ceil(k / 64)                                      */
+    uint32_t spin_limit;     /* polls of a ready flag before counting a timeout   */
+    uint32_t reserved[3];    /* pads the block to 144 bytes (whole 16-byte words) */
+} T0gGemmSkArgs;
+
+#define T0G_SK_TILE 256u
+#define T0G_SK_SLOT_BYTES (T0G_SK_TILE * T0G_SK_TILE * 4u)
+#define T0G_SK_CTL_WORDS 16u
+#define T0G_SK_TICKET 0u         /* control word: next logical workgroup id           */
+#define T0G_SK_DONE 1u           /* control word: finished workgroups                 */
+#define T0G_SK_TIMEOUTS 2u       /* control word: ready-flag waits that gave up, and
+                                    workgroups that drew a ticket past the grid       */
+
+#if defined(__HIPCC__)
+#define T0G_HD __host__ __device__
+#else
+#define T0G_HD
+#endif
+/* First iteration of logical workgroup w (w = grid gives the total): the first
+ * total % grid workgroups get one iteration more. */
+static inline T0G_HD uint32_t t0g_sk_begin(uint32_t total, uint32_t grid, uint32_t w) {
+    const uint32_t base = total / grid, rem = total % grid;
+    return w * base + (w < rem ? w : rem);
+}
+/* Logical workgroup whose range holds iteration `it` (requires total >= grid). */
+static inline T0G_HD uint32_t t0g_sk_worker(uint32_t total, uint32_t grid, uint32_t it) {
+    const uint32_t base = total / grid, rem = total % grid, split = rem * (base + 1u);
+    return it < split ? it / (base + 1u) : rem + (it - split) / base;
+}
+
 typedef struct T0gReduceArgs {
     uint64_t ws;             /* f32 planes [splits][m][ldw]                       */
     uint64_t c;              /* output (f32 or bf16) [m][ldc]                     */

@@ -72,6 +72,8 @@ struct t0g_device {
     size_t ws_bytes = 0;
     uint64_t conv = 0;         // bf16 operand scratch of the matmul entry points
     size_t conv_bytes = 0;
+    uint32_t num_cus = 0;      // compute units: the stream-K grid
+    uint64_t sk_sync = 0;      // stream-K control words and ready flags (zero between launches)
 };
 
 namespace t0g {
@@ -176,8 +178,19 @@ struct GemmPlan {
     uint32_t k_per_split;
     uint32_t tiles_m, tiles_n;
     uint32_t wg;   // threads per workgroup of the chosen kernel
+    bool stream_k;
+    uint32_t sk_ipt;   // stream-K: 64-wide K steps per tile
     std::string symbol;
 };
+
+// Stream-K grid: one workgroup per CU (at most 256, the table's CU count),
+// never more than there are (tile, K step) pairs.
+static uint32_t sk_grid(const GemmPlan &p, uint32_t num_cus) {
+    const uint64_t total = (uint64_t)p.tiles_m * p.tiles_n * p.sk_ipt;
+    uint64_t g = num_cus ? num_cus : kNumCUs;
+    if (g > kNumCUs) g = kNumCUs;
+    return (uint32_t)(total < g ? total : g);
+}
 
 // The fast kernels need 16-byte aligned rows and operands under 2 GiB (their
 // buffer descriptors use 0x80000000 as the always-out-of-range offset).
@@ -194,7 +207,12 @@ static bool operands_aligned(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uin
 
 static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, bool aligned, uint32_t m, uint32_t n,
                      uint32_t k, uint32_t split_req, GemmPlan *p) {
+    bool stream_k = split_req == T0G_STREAM_K;
+    if (stream_k) split_req = 1;
     if (!aligned && tile->bm == 256) tile = &kTiles[1];   // no element-wise-load variant of the 256x256 tile
+    if (tile->bm != 256 || k == 0) stream_k = false;      // the data-parallel kernel then
+    p->stream_k = stream_k;
+    p->sk_ipt = stream_k ? (k + kTileK - 1) / kTileK : 0;
     p->tile = tile;
     p->transpose = transpose;
     p->out_bf16 = out_bf16;
@@ -226,9 +244,12 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, boo
     // faster.
     p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
-                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (deep ? "_d" : "") : "_u");
+                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (deep ? "_d" : "") : "_u") +
+                (stream_k ? "_sk" : "");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
+    if (stream_k && (uint64_t)p->tiles_m * p->tiles_n * p->sk_ipt > 0x7FFFFFFFull)
+        return fail(T0G_ERR_INVALID_ARG, "stream-K: too many (tile, K step) pairs for %ux%ux%u", m, n, k);
     return T0G_OK;
 }
 
@@ -263,6 +284,28 @@ struct GemmOperands {
     float epi_scale, clamp_lo, clamp_hi;
     uint64_t c_split_stride;   // reference-layout path: caller-owned planes
 };
+
+// Polls of a stream-K ready flag (each followed by a short s_sleep: about a
+// tenth of a second in all, against microseconds for a real wait) before a
+// workgroup gives up and counts a timeout.
+constexpr uint32_t kSkSpinLimit = 1u << 20;
+
+// Stream-K control words and ready flags, allocated and zeroed once per device;
+// every launch leaves them zero again.
+static int ensure_sk_sync(t0g_device *dev) {
+    if (dev->sk_sync) return T0G_OK;
+    const size_t bytes = (T0G_SK_CTL_WORDS + kNumCUs) * 4;
+    void *ptr = nullptr;
+    hipError_t e = T0G_HIP(hipMalloc(&ptr, bytes));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(stream-K flags)");
+    e = T0G_HIP(hipMemsetAsync(ptr, 0, bytes, dev->stream));
+    if (e != hipSuccess) {
+        (void)hipFree(ptr);
+        return hip_fail(e, "hipMemsetAsync(stream-K flags)");
+    }
+    dev->sk_sync = (uint64_t)ptr;
+    return T0G_OK;
+}
 
 // Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
 // the partial planes go to `ws` and the reduce kernel produces C.
@@ -304,6 +347,17 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     const uint64_t esize = reduce || !p.out_bf16 ? 4 : 2;
     if ((args.c & 15) == 0 && ((uint64_t)args.ldc * esize) % 16 == 0 && args.c_split_stride % 16 == 0)
         args.flags |= T0G_FLAG_C_VEC;
+    if (p.stream_k) {
+        T0gGemmSkArgs sa;
+        memset(&sa, 0, sizeof sa);
+        sa.g = args;
+        sa.partials = ws;
+        sa.sync = dev->sk_sync;
+        sa.grid = sk_grid(p, dev->num_cus);
+        sa.iters_per_tile = p.sk_ipt;
+        sa.spin_limit = kSkSpinLimit;
+        return launch(dev, f, sa.grid, 1, 1, p.wg, &sa, sizeof sa);
+    }
     rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.wg, &args, sizeof args);
     if (rc || !reduce) return rc;
 
@@ -377,7 +431,10 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
     if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
     if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
     const uint32_t sk = d->split_k ? d->split_k : cfg_split(cfg);
-    if (sk > kMaxSplitK) return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u > %u", sk, kMaxSplitK);
+    if (sk == T0G_STREAM_K && (cfg->tile_m != 256 || cfg->tile_n != 256))
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the 256x256 tile");
+    if (sk > kMaxSplitK && sk != T0G_STREAM_K)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u > %u", sk, kMaxSplitK);
     const TileDef *tile = find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
     const bool aligned = operands_aligned(d->a, d->b, d->m, d->n, d->k, o->lda, o->ldb, t);
     return make_plan(tile, t, d->out_dtype == T0G_BF16, aligned, d->m, d->n, d->k, sk, plan);
@@ -388,6 +445,20 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
 using namespace t0g;
 
 extern "C" {
+
+int t0g_stream_k_timeouts(t0g_device *dev, uint32_t *count) {
+    if (!dev || !count) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    *count = 0;
+    if (!dev->sk_sync) return ok();
+    if ((rc = wait_stream(dev))) return rc;
+    hipError_t e = T0G_HIP(hipMemcpy(count, (const void *)(dev->sk_sync + 4 * T0G_SK_TIMEOUTS), 4,
+                                     hipMemcpyDeviceToHost));
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(stream-K timeouts)");
+    return ok();
+}
 
 int t0g_debug_fail_hip_call(int n) {
     if (n < 0) return fail(T0G_ERR_INVALID_ARG, "n must be >= 0");
@@ -431,6 +502,7 @@ int t0g_device_open(int ordinal, t0g_device **out) {
                     prop.gcnArchName);
     std::unique_ptr<t0g_device> dev(new t0g_device);
     dev->ordinal = ordinal;
+    dev->num_cus = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : kNumCUs;
     if ((e = T0G_HIP(hipStreamCreateWithFlags(&dev->own_stream, hipStreamNonBlocking))) != hipSuccess)
         return hip_fail(e, "hipStreamCreate");
     dev->stream = dev->own_stream;
@@ -448,6 +520,7 @@ int t0g_device_close(t0g_device *dev) {
     if (!dev->poisoned) (void)hipStreamSynchronize(dev->stream);
     if (dev->ws) (void)hipFree((void *)dev->ws);
     if (dev->conv) (void)hipFree((void *)dev->conv);
+    if (dev->sk_sync) (void)hipFree((void *)dev->sk_sync);
     for (uint64_t a : dev->allocations) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
@@ -551,6 +624,8 @@ static int kernel_get_common(t0g_device *dev, const t0g_gemm_config *cfg, Kernel
     *out = nullptr;
     int rc = validate(cfg);
     if (rc) return rc;
+    if (cfg->split_k == T0G_STREAM_K)
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K configs run through t0g_gemm only");
     if ((rc = check_chain(chain))) return rc;
     if (chain && cfg->epilogue != T0G_EPI_STORE_F32)
         return fail(T0G_ERR_INVALID_ARG, "an epilogue chain replaces cfg->epilogue, which must be STORE_F32");
@@ -779,7 +854,10 @@ int t0g_gemm_workspace_size(const t0g_gemm_desc *d, size_t *bytes) {
     GemmOperands o;
     int rc = resolve_desc(d, &cfg, &p, &o);
     if (rc) return rc;
-    *bytes = p.splits > 1 ? (size_t)p.splits * d->m * d->n * 4 : 0;
+    if (p.stream_k)
+        *bytes = (size_t)sk_grid(p, kNumCUs) * T0G_SK_SLOT_BYTES;
+    else
+        *bytes = p.splits > 1 ? (size_t)p.splits * d->m * d->n * 4 : 0;
     return ok();
 }
 
@@ -804,8 +882,10 @@ static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d) {
     if ((rc = check_usable(dev))) return rc;
     if (d->m == 0 || d->n == 0) return ok();
     uint64_t ws = 0;
-    if (p.splits > 1) {
-        const size_t need = (size_t)p.splits * d->m * d->n * 4;
+    if (p.stream_k && (rc = ensure_sk_sync(dev))) return rc;
+    if (p.splits > 1 || p.stream_k) {
+        const size_t need = p.stream_k ? (size_t)sk_grid(p, dev->num_cus) * T0G_SK_SLOT_BYTES
+                                       : (size_t)p.splits * d->m * d->n * 4;
         if (d->workspace) {
             if (d->workspace_bytes < need)
                 return fail(T0G_ERR_INVALID_ARG, "workspace of %llu bytes, split-K needs %zu",

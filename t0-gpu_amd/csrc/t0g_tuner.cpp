@@ -348,6 +348,15 @@ void candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, std::vec
             all.push_back(c);
         }
     }
+    {
+        // stream-K, ranked with the margin auto_select demands of it
+        Cand c;
+        c.t = model_time_sk_us(m, k, n) / 0.85;
+        c.order = order++;
+        make_config(kTiles[0], T0G_STREAM_K, &c.cfg);
+        c.cfg.transpose = transpose;
+        all.push_back(c);
+    }
     std::stable_sort(all.begin(), all.end(), [](const Cand &a, const Cand &b) { return a.t < b.t; });
     out->clear();
     for (const Cand &c : all) out->push_back(c.cfg);
@@ -393,7 +402,9 @@ int tune_locked(t0g_tuner *t, t0g_device *dev, const TuneKey &key, const TuneEnt
         // clock of a power-limited MI355X needs that long under load to settle,
         // and a ranking taken at an unsettled clock favours whoever runs later.
         const TileDef *tile = find_tile(cands[i].tile_m, cands[i].tile_n, cands[i].tile_k, cands[i].wg_size);
-        const double model_us = tile ? model_time_us(*tile, key.m, key.k, key.n, cfg_split(&cands[i])) : 100.0;
+        const double model_us = cands[i].split_k == T0G_STREAM_K ? model_time_sk_us(key.m, key.k, key.n)
+                                : tile ? model_time_us(*tile, key.m, key.k, key.n, cfg_split(&cands[i]))
+                                       : 100.0;
         const uint32_t warm = (uint32_t)std::min(500.0, std::max(2.0, 10000.0 / std::max(model_us, 1.0)));
         std::vector<double> ms;
         int brc = time_gemm(dev, &d, warm, t->n_iters, &ms);

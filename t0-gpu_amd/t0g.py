@@ -40,6 +40,7 @@ NT, NN, TN, TT = 0, 1, 2, 3
 LAYOUTS = {"NT": NT, "NN": NN, "TN": TN, "TT": TT}
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
 F32, BF16 = 0, 1
+STREAM_K = 0x80000000   # GemmConfig.split_k value selecting the stream-K schedule
 # tile_ir EpilogueOp (src/t0/tile_ir.rs:41-62): the fused epilogue chain
 OP_BIAS_ADD, OP_SCALE, OP_RELU, OP_SILU, OP_GELU, OP_ABS, OP_NEG, OP_CLAMP = range(1, 9)
 EPILOGUE_OPS = {"bias": OP_BIAS_ADD, "scale": OP_SCALE, "relu": OP_RELU, "silu": OP_SILU,
@@ -243,6 +244,9 @@ _sig("t0g_tuner_invalidate", ctypes.c_int, _p, _u32, _u32, _u32, _u32, _u32)
 _sig("t0g_tuner_clear", ctypes.c_int, _p)
 _sig("t0g_tuner_report", ctypes.c_int, _p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_auto_gemm", ctypes.c_int, _p, _p, _u64, _u64, _u64, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_double))
+_sig("t0g_stream_k_begin", _u32, _u32, _u32, _u32)
+_sig("t0g_stream_k_worker", _u32, _u32, _u32, _u32)
+_sig("t0g_stream_k_timeouts", ctypes.c_int, _p, _u32p)
 _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 
@@ -459,6 +463,11 @@ class GpuRuntime:
 
     def __exit__(self, *exc):
         self.close()
+
+    def stream_k_timeouts(self):
+        v = ctypes.c_uint32()
+        _check(_lib.t0g_stream_k_timeouts(self.handle, ctypes.byref(v)))
+        return v.value
 
     def set_stream(self, hip_stream_ptr):
         _check(_lib.t0g_device_set_stream(self.handle, ctypes.c_void_p(hip_stream_ptr or None)))
@@ -718,3 +727,13 @@ def auto_gemm(rt, a, b, c, m, n, k, tuner=None):
     tf = ctypes.c_double()
     _check(_lib.t0g_auto_gemm(tuner.handle if tuner is not None else None, rt.handle, a, b, c, m, n, k, ctypes.byref(tf)))
     return tf.value
+
+
+def stream_k_begin(total, grid, w):
+    """First (tile, K step) pair of stream-K workgroup w (w = grid: the total)."""
+    return _lib.t0g_stream_k_begin(total, grid, w)
+
+
+def stream_k_worker(total, grid, it):
+    """The stream-K workgroup whose range holds pair `it`."""
+    return _lib.t0g_stream_k_worker(total, grid, it)

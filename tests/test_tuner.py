@@ -202,7 +202,8 @@ def test_candidates_start_with_auto_select(m, n, k):
     for c in cands:
         c.validate()
         sk = max(1, c.split_k)
-        assert sk == 1 or k >= sk * 4 * 64
+        assert sk == 1 or sk == t0g.STREAM_K or k >= sk * 4 * 64
+    assert sum(c.split_k == t0g.STREAM_K for c in cands) == 1
     assert len(t0g.tune_candidates(m, n, k, "NT", 3)) == min(3, len(cands))
     assert all(c.transpose == t0g.TN for c in t0g.tune_candidates(m, n, k, "TN", 8))
 
@@ -210,4 +211,4 @@ def test_candidates_start_with_auto_select(m, n, k):
 def test_candidates_cover_every_tile():
     cands = t0g.tune_candidates(4096, 4096, 4096, "NT", 64)
     assert {(c.tile_m, c.tile_n) for c in cands} == {(256, 256), (128, 128), (64, 64)}
-    assert len(cands) == 3 * 5   # 3 tiles x split 1..16 (K = 4096 is 64 K tiles, >= 4 per split)
+    assert len(cands) == 3 * 5 + 1   # 3 tiles x split 1..16 (64 K tiles, >= 4 per split), and stream-K
