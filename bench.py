@@ -215,6 +215,33 @@ def stream_k_extra(t0g, torch, rt, stream, steps, warmup):
     return out
 
 
+def cold_gemm(t0g, torch, rt, stream, m, n, k, layout, trials):
+    """One GEMM per trial after a 512 MB device copy that evicts the GEMM's operands from
+    the 256 MB Infinity Cache and the L2s; each launch timed alone by HIP events; median."""
+    a, b = make_inputs(torch, m, n, k, layout, 2)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    flush_src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    flush_dst = torch.empty_like(flush_src)
+    desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16)
+    for _ in range(3):
+        rt.gemm_desc(desc)
+    times = []
+    for _ in range(trials):
+        flush_dst.copy_(flush_src)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rt.gemm_desc(desc)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    ms = times[len(times) // 2]
+    return {"us_median": round(ms * 1e3, 2), "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1),
+            "frac_of_peak": round(2.0 * m * n * k / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
+            "us_min": round(times[0] * 1e3, 2), "trials": trials, "kernel": t0g.gemm_kernel_name(desc)}
+
+
 def cpu_baseline(torch, tensors, m, n, k, min_seconds):
     """The CPU oracle (oracle/ref_gemm.c, a bit-exact restatement of the reference's
     CPU GEMM) on this host: the whole 4096^3 product, repeated to ~min_seconds."""
@@ -237,7 +264,13 @@ def cpu_baseline(torch, tensors, m, n, k, min_seconds):
     oracle.gemm_nt_naive(a_np, np.ascontiguousarray(b_np.T), m, k, n, rows=(0, rows))
     t_naive = time.perf_counter() - t0
     naive = 2.0 * rows * n * k / t_naive / 1e12
-    return {"value": fast, "unit": "TFLOPS", "cores": threads, "kind": "port",
+    cpu_model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+    except OSError:
+        pass
+    return {"value": fast, "unit": "TFLOPS", "cores": threads, "kind": "port", "cpu_model": cpu_model,
             "sample": f"full {m}x{n}x{k} NN product x{reps} ({t_total:.1f} s, vectorised + OpenMP, "
                       f"bit-identical to the reference loop)",
             "naive_single_thread": {"value": naive, "unit": "TFLOPS", "cores": 1,
@@ -293,6 +326,19 @@ def main():
         rt.close()
         return
 
+    if args.only and args.only.upper().startswith("CONVERT:"):
+        n_el = int(float(args.only.split(":")[1]) * (1 << 20)) // 8 * 8
+        src = torch.randn(n_el, device="cuda")
+        dst = torch.empty(n_el, dtype=torch.bfloat16, device="cuda")
+        ms = _event_ms(torch, stream, lambda: rt.f32_to_bf16(src.data_ptr(), dst.data_ptr(), n_el), args.steps,
+                       args.warmup)
+        print(json.dumps({"only": args.only, "kernel": "t0g_f32_to_bf16_rne", "elements": n_el,
+                          "us_per_launch": round(ms * 1e3, 2), "gbs": round(6.0 * n_el / (ms * 1e-3) / 1e9, 1)}),
+              flush=True)
+        rt.set_stream(None)
+        rt.close()
+        return
+
     if args.only:
         lay, m, n, k = args.only.split(":")
         m, n, k = int(m), int(n), int(k)
@@ -340,6 +386,8 @@ def main():
     if not args.no_extra:
         extra = {}
         steps8 = max(5, args.steps // 2)
+        log("[bench] 4096^3 NN bf16, operands evicted from the caches before each launch")
+        extra["gemm_nn_4096^3_cold_cache"] = cold_gemm(t0g, torch, rt, stream, M, N, K, "NN", 25)
         log(f"[bench] 8192^3 NN bf16: steps {steps8}")
         r8 = time_gemm(t0g, torch, rt, stream, 8192, 8192, 8192, "NN", steps8, max(3, args.warmup // 8), seed=4)
         t8 = r8["flop"] / (r8["event_ms_per_launch"] * 1e-3) / 1e12
