@@ -714,3 +714,28 @@ def test_linear_regression_training_reduces_loss(rt, bufs):
             check_parity(g, ref, m, "dW step 0")
         w = w - 2.0 * g
     assert losses[-1] < losses[0] * 0.1, losses
+
+
+# ---- the largest operands ---------------------------------------------------
+@pytest.fixture(scope="module")
+def big_a():
+    """2^30 random bf16 values (2 GiB): A of up to 65536 x 16384 (or 16384 x 65536)."""
+    return o.rand_bf16_xorshift(1 << 30, 99)
+
+
+@pytest.mark.parametrize("layout,m,path", [("NT", 65528, "fast"), ("NT", 65536, "generic"),
+                                           ("TN", 65528, "fast"), ("TN", 65536, "generic")])
+def test_largest_operands(rt, bufs, big_a, layout, m, path):
+    """A just below 2^30 elements runs on the fast kernels with offsets reaching 2 GiB;
+    exactly 2^30 goes to the element-wise kernels; both checked on oracle rows taken up
+    to the last row (K-contiguous A for NT, M-contiguous A for TN)."""
+    k, n = 16384, 256
+    _log(f"[case] largest operands {layout} {m}x{n}x{k} ({path})")
+    a_st = big_a[: m * k]
+    b_st = o.rand_bf16_xorshift(n * k, 7)
+    desc = t0g.gemm_desc(0, 0, 0, m, n, k, transpose=layout)
+    assert t0g.gemm_kernel_name(desc).endswith("_u") == (path == "generic")
+    c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k)
+    rows = np.array([0, 1, 255, 256, m // 2 + 3, m - 257, m - 2, m - 1])
+    ref = o.gemm_rows(layout, a_st, b_st, m, n, k, rows)
+    check_parity(c[rows], ref, k, f"largest {layout} {m}x{n}x{k}")

@@ -210,3 +210,23 @@ def test_desc_chain_validation():
     d = t0g.gemm_desc(0x1000, 0x2000, 0x3000, 256, 256, 256, transpose="NN", epilogue_ops=["gelu", "clamp"],
                       clamp=(-1.0, 1.0))
     assert t0g.gemm_kernel_name(d).startswith("t0g_gemm_")
+
+
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+def test_operand_size_limits(layout):
+    """The fast kernels address each operand with 32-bit buffer offsets: operands below
+    2^30 elements take them, larger ones the element-wise kernel (32-bit element offsets),
+    and 2^31 elements or more are refused with an error instead of overflowing."""
+    k, n = 16384, 256
+    a, b = 1 << 12, 1 << 40   # 16-byte aligned device addresses (not dereferenced here)
+
+    def name(m):
+        return t0g.gemm_kernel_name(t0g.gemm_desc(a, b, 0, m, n, k, transpose=layout, out_dtype=t0g.BF16))
+
+    below = (1 << 30) // k - 8   # a multiple of 8: M-contiguous rows stay 16-byte aligned
+    assert name(below).startswith("t0g_gemm_256x256_k64_") and not name(below).endswith("_u")   # below 2^30
+    assert name((1 << 30) // k).endswith("_u")                                    # exactly 2^30
+    assert name((1 << 31) // k - 1).endswith("_u")
+    with pytest.raises(t0g.T0gError) as e:
+        name((1 << 31) // k)                                                      # 2^31 elements
+    assert e.value.code == t0g.ERR_INVALID_ARG
