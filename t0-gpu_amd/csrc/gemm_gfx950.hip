@@ -566,6 +566,25 @@ __device__ __forceinline__ u32x4_t rsrc_words(uint64_t base, uint32_t bytes, uin
     return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
 }
 
+// Wide form of rsrc_words for operands of any size: [base + shift, base + bytes)
+// cut to its first 2 GiB (kOob stays out of range).  Callers shift it to the
+// tile's first row (K-contiguous operands) or the stage's first k row
+// (M/N-contiguous operands), so that every offset they use from there is below
+// 2 GiB; the host checks the leading dimensions for that.
+__device__ __forceinline__ u32x4_t rsrc_words_wide(uint64_t base, uint64_t bytes, uint64_t shift) {
+    const uint64_t left = shift < bytes ? bytes - shift : 0u;
+    const uint32_t rec = left < (uint64_t)kOob ? (uint32_t)left : kOob;
+    const uint64_t a = base + shift;
+    return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
+}
+
+// Bytes spanned by an operand of `rows` M/N rows and k K values with leading
+// dimension ld: K-contiguous [rows][ld] or M/N-contiguous [k][ld].
+template <bool K_MAJOR>
+__device__ __forceinline__ uint64_t operand_bytes_wide(uint32_t rows, uint32_t k, uint32_t ld) {
+    return K_MAJOR ? ((uint64_t)(rows - 1) * ld + k) * 2 : ((uint64_t)(k - 1) * ld + rows) * 2;
+}
+
 // 16-byte buffer load straight into LDS: lane l's data goes to LDS address
 // m0 + 16 * l.  An SALU write of M0 needs one wait state before an LDS-DMA
 // instruction reads it, hence the s_nop.  Completion is tracked by vmcnt only
@@ -1166,6 +1185,25 @@ extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvert
     T0G_GEMM_256(t0g_gemm_256x256_k64_tt_##OUTN, false, true, OBF)
 T0G_GEMM_LAYOUTS_256(f32, false)
 T0G_GEMM_LAYOUTS_256(bf16, true)
+
+// The same kernels for operands of 2^30 elements or more (suffix _x): buffer
+// descriptors rebased per tile (K-contiguous operands) or per K stage
+// (M/N-contiguous), 64-bit byte counts.
+#define T0G_GEMM_256_X(NAME, AK, BKM, OBF)                                                                \
+    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
+        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmArgs p) {                \
+        if constexpr (AK)                                                                                 \
+            t0g::gemm_tile_pp<AK, BKM, OBF, true>(p);                                                    \
+        else                                                                                              \
+            t0g::gemm_tile_fast16<AK, BKM, OBF, true>(p);                                                \
+    }
+#define T0G_GEMM_LAYOUTS_256_X(OUTN, OBF)                                   \
+    T0G_GEMM_256_X(t0g_gemm_256x256_k64_nt_##OUTN##_x, true, true, OBF)     \
+    T0G_GEMM_256_X(t0g_gemm_256x256_k64_nn_##OUTN##_x, true, false, OBF)    \
+    T0G_GEMM_256_X(t0g_gemm_256x256_k64_tn_##OUTN##_x, false, false, OBF)   \
+    T0G_GEMM_256_X(t0g_gemm_256x256_k64_tt_##OUTN##_x, false, true, OBF)
+T0G_GEMM_LAYOUTS_256_X(f32, false)
+T0G_GEMM_LAYOUTS_256_X(bf16, true)
 
 // The same tiles on a stream-K schedule (suffix _sk, T0gGemmSkArgs).
 #define T0G_GEMM_256_SK(NAME, AK, BKM, OBF)                                                               \

@@ -14,6 +14,8 @@
 #ifndef T0G_GEMM_MFMA16_H
 #define T0G_GEMM_MFMA16_H
 
+#include <type_traits>
+
 namespace t0g {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -40,7 +42,10 @@ __device__ __forceinline__ void dma16_add(u32x4_t rsrc, uint32_t voff, uint32_t 
         : "memory", "m0");
 }
 
-template <bool K_MAJOR, int ROWS, int NT, int SUBS>
+// WIDE: operands of any size (buffer descriptors rebased per tile or stage and
+// cut to 2 GiB, 64-bit byte counts); otherwise operands below 2^30 elements,
+// addressed from the operand base with 32-bit byte counts.
+template <bool K_MAJOR, int ROWS, int NT, int SUBS, bool WIDE = false>
 struct Op16;
 
 // K-contiguous operand of a 256-row tile, 64 K values per stage: 128-byte LDS
@@ -48,14 +53,16 @@ struct Op16;
 // 8 (i W + wave) + lane / 8 (W waves); for even W, fk<64> of those rows does not
 // depend on i, so one offset register and one K column serve all of a wave's
 // instructions.
-template <int ROWS, int NT, int SUBS>
-struct Op16<true, ROWS, NT, SUBS> {
+template <int ROWS, int NT, int SUBS, bool WIDE>
+struct Op16<true, ROWS, NT, SUBS, WIDE> {
+    typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
     static constexpr int kWaves = NT / 64;
     static constexpr uint32_t kKRow = 128;
     static constexpr int kInstr = ROWS * kKRow / 1024 / kWaves;
     static_assert(ROWS == 256 && (kWaves == 4 || kWaves == 8), "offset sharing assumes a 256-row tile, 4 or 8 waves");
     static constexpr uint32_t kStageBytes = ROWS * kKRow;
-    uint32_t off0;    // byte offset of instruction 0's piece at k = 0
+    uint64_t rowb;    // WIDE: byte offset of the tile's first row in the operand
+    uint32_t off0;    // byte offset of instruction 0's piece at k = 0 (WIDE: from the tile's first row)
     uint32_t kcol;    // first K column of the lane's piece
     uint32_t step;    // bytes between instructions (8 W rows)
     uint32_t wave;
@@ -67,14 +74,23 @@ struct Op16<true, ROWS, NT, SUBS> {
         const uint32_t r = 8 * wave + (lane >> 3);
         const uint32_t c = (lane & 7u) ^ fk<64>(r);
         kcol = c * 8;
-        off0 = ((row0 + r) * ld + c * 8) * 2;
+        if constexpr (WIDE) {
+            rowb = (uint64_t)row0 * ld * 2;
+            off0 = (r * ld + c * 8) * 2;
+        } else {
+            rowb = 0;
+            off0 = ((row0 + r) * ld + c * 8) * 2;
+        }
         step = 16 * kWaves * ld;
         const uint32_t row = wrow + (lane & 15u), qk = lane >> 4;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) frag[kk] = row * kKRow + (((4u * kk + qk) ^ fk<64>(row)) << 4);
     }
-    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t, uint32_t k0) const {
-        return rsrc_words(base, bytes, (uint64_t)k0 * 2);
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, bytes_t bytes, uint32_t, uint32_t k0) const {
+        if constexpr (WIDE)
+            return rsrc_words_wide(base + rowb, bytes > rowb ? bytes - rowb : 0u, (uint64_t)k0 * 2);
+        else
+            return rsrc_words(base, bytes, (uint64_t)k0 * 2);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
@@ -85,7 +101,7 @@ struct Op16<true, ROWS, NT, SUBS> {
             dma16_add(r, off0, i * step, m0);
     }
     template <bool CHECK>
-    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
         const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
@@ -103,8 +119,9 @@ struct Op16<true, ROWS, NT, SUBS> {
 // 2 (i W + wave) + lane / 32 (W waves); their swizzle depends on i only through
 // bit 0 of i (W = 4) or not at all (W = 8), so two offset registers serve all
 // of a wave's instructions.
-template <int ROWS, int NT, int SUBS>
-struct Op16<false, ROWS, NT, SUBS> {
+template <int ROWS, int NT, int SUBS, bool WIDE>
+struct Op16<false, ROWS, NT, SUBS, WIDE> {
+    typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
     static constexpr int kWaves = NT / 64;
     static constexpr uint32_t kRowB = ROWS * 2;
     static constexpr uint32_t kGranules = ROWS / 16;
@@ -138,8 +155,11 @@ struct Op16<false, ROWS, NT, SUBS> {
         const uint32_t k0 = 8 * q + r, f = fm16(k0, kGranules);
         frag0 = k0 * kRowB + c * 8 + (((wrow >> 4) ^ f) << 5);
     }
-    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
-        return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+    __device__ __forceinline__ u32x4_t rsrc(uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0) const {
+        if constexpr (WIDE)
+            return rsrc_words_wide(base, bytes, (uint64_t)k0 * ld * 2);
+        else
+            return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
@@ -150,7 +170,7 @@ struct Op16<false, ROWS, NT, SUBS> {
             dma16_add(r, off[i & 1], i * step, m0);
     }
     template <bool CHECK>
-    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0,
+    __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
                                           uint32_t kend) const {
         const u32x4_t r = rsrc(base, bytes, ld, k0);
 #pragma unroll
@@ -278,7 +298,8 @@ __device__ __forceinline__ void mfma16_rows(f32x4_t (&acc)[SM][SN], const bf16x8
 // and reads no memory.
 template <bool CHECK, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
-                                             const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg,
+                                             const T0gGemmArgs& p, typename OpA::bytes_t a_bytes,
+                                             typename OpB::bytes_t b_bytes, uint32_t kbeg,
                                              uint32_t kend, int nst, uint32_t lds0) {
     constexpr int kHalf = OpA::kInstr;   // the A half of a stage's DMA, then the B half
     static_assert(OpA::kInstr == OpB::kInstr, "equal A and B halves");
@@ -287,7 +308,7 @@ __device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& 
     lb.template issue<CHECK>(lds0 + A_BYTES, p.b, b_bytes, p.ldb, kbeg, kend);
     {
         const uint32_t k1 = kbeg + 64;
-        la.template issue<CHECK>(lds0 + STAGE, p.a, k1 < kend ? a_bytes : 0u, p.lda, k1, kend);
+        la.template issue<CHECK>(lds0 + STAGE, p.a, k1 < kend ? a_bytes : typename OpA::bytes_t{0}, p.lda, k1, kend);
     }
     T0G_WAIT_VMCNT(kHalf);
     barrier_no_fence();
@@ -301,8 +322,8 @@ __device__ __forceinline__ void k_pipeline16(f32x4_t (&acc)[SM][SN], const OpA& 
     for (int s = 0; s < nst; ++s) {
         const uint32_t nxt = cur ^ STAGE;
         const uint32_t k1 = kbeg + (uint32_t)(s + 1) * 64, k2 = k1 + 64;
-        const u32x4_t rb1 = lb.rsrc(p.b, k1 < kend ? b_bytes : 0u, p.ldb, k1);
-        const u32x4_t ra2 = la.rsrc(p.a, k2 < kend ? a_bytes : 0u, p.lda, k2);
+        const u32x4_t rb1 = lb.rsrc(p.b, k1 < kend ? b_bytes : typename OpB::bytes_t{0}, p.ldb, k1);
+        const u32x4_t ra2 = la.rsrc(p.a, k2 < kend ? a_bytes : typename OpA::bytes_t{0}, p.lda, k2);
         mfma16_rows<0, kHalf, kHalf, CHECK, 0, SM, 0>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt,
                                                      lds0 + nxt, ra2, rb1, k1, kend);
         mfma16_rows<1, 0, 0, CHECK, 0, kHalfRows, kHalfRows>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt,
@@ -475,14 +496,14 @@ __device__ __forceinline__ void tile_origin(const T0gGemmArgs& p, uint32_t& m0, 
 }
 
 // The 256x256 fast path on 16x16x32 MFMAs (2 x 2 waves of 128 x 128).
-template <bool A_K, bool B_K, bool OUT_BF16>
+template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false>
 __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
     constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 2;
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 16, SN = WTN / 16;
-    using OpA = Op16<A_K, BM, NT, SM>;
-    using OpB = Op16<B_K, BN, NT, SN>;
+    using OpA = Op16<A_K, BM, NT, SM, WIDE>;
+    using OpB = Op16<B_K, BN, NT, SN, WIDE>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
     constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
@@ -495,8 +516,15 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
     const int nst = kend > kbeg ? (int)((kend - kbeg + 63) / 64) : 0;
 
-    const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
-    const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+    typename OpA::bytes_t a_bytes;
+    typename OpB::bytes_t b_bytes;
+    if constexpr (WIDE) {
+        a_bytes = operand_bytes_wide<A_K>(p.m, p.k, p.lda);
+        b_bytes = operand_bytes_wide<B_K>(p.n, p.k, p.ldb);
+    } else {
+        a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+        b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+    }
 
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -550,7 +578,8 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
 // half of the CU's DMA requests for the stage.
 template <bool CHECK, uint32_t A_BYTES, uint32_t STAGE, int SM, int SN, class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline_pp(f32x4_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
-                                              const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes,
+                                              const T0gGemmArgs& p, typename OpA::bytes_t a_bytes,
+                                              typename OpB::bytes_t b_bytes,
                                               uint32_t kbeg, uint32_t kend, int nst, uint32_t lds0, uint32_t group) {
     bf16x8_t fa[SM], fb[SN];
     la.template issue<CHECK>(lds0, p.a, a_bytes, p.lda, kbeg, kend);
@@ -604,14 +633,14 @@ __device__ __forceinline__ void k_pipeline_pp(f32x4_t (&acc)[SM][SN], const OpA&
 
 // The 256x256 tile with 8 waves (2 x 4 of 128 x 64) in ping-pong: two waves per
 // SIMD, 128 accumulators each.
-template <bool A_K, bool B_K, bool OUT_BF16>
+template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false>
 __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
     constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4;
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 16, SN = WTN / 16;
-    using OpA = Op16<A_K, BM, NT, SM>;
-    using OpB = Op16<B_K, BN, NT, SN>;
+    using OpA = Op16<A_K, BM, NT, SM, WIDE>;
+    using OpB = Op16<B_K, BN, NT, SN, WIDE>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
@@ -621,8 +650,15 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
     const uint32_t kbeg = blockIdx.y * p.k_per_split;
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
     const int nst = kend > kbeg ? (int)((kend - kbeg + 63) / 64) : 0;
-    const uint32_t a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
-    const uint32_t b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+    typename OpA::bytes_t a_bytes;
+    typename OpB::bytes_t b_bytes;
+    if constexpr (WIDE) {
+        a_bytes = operand_bytes_wide<A_K>(p.m, p.k, p.lda);
+        b_bytes = operand_bytes_wide<B_K>(p.n, p.k, p.ldb);
+    } else {
+        a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
+        b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
+    }
 
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;

@@ -192,25 +192,41 @@ static uint32_t sk_grid(const GemmPlan &p, uint32_t num_cus) {
     return (uint32_t)(total < g ? total : g);
 }
 
-// The fast kernels need 16-byte aligned rows and operands under 2 GiB (their
-// buffer descriptors use 0x80000000 as the always-out-of-range offset).
-static bool operands_aligned(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
-                             uint32_t t) {
-    if ((a & 15) || (b & 15) || (lda & 7) || (ldb & 7)) return false;
+// How the kernels address the operands.
+//   Fast: 16-byte aligned rows and operands below 2^30 elements; the buffer
+//     descriptors span the whole operand (0x80000000 is their always-out-of-range
+//     offset).
+//   Wide: aligned operands of 2^30 elements or more, 256x256 kernels only (_x):
+//     the descriptors are rebased to the tile's first row (K-contiguous operand)
+//     or the stage's first k row (M/N-contiguous) and cut to 2 GiB; the offsets
+//     used from there stay below 2 GiB for leading dimensions below these bounds
+//     (256 rows of a K-contiguous tile; 64 k rows plus one row of a stage).
+//   Elementwise: everything else (_u kernels, 32-bit element offsets).
+enum class OperandPath { Fast, Wide, Elementwise };
+constexpr uint32_t kMaxKMajorLd = 1u << 22;
+constexpr uint32_t kMaxMnMajorLd = (1u << 24) - 256;
+
+static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uint32_t k, uint32_t lda,
+                                uint32_t ldb, uint32_t t) {
+    if ((a & 15) || (b & 15) || (lda & 7) || (ldb & 7)) return OperandPath::Elementwise;
+    if (a_k_major(t) ? (k & 7) != 0 : ((m & 7) != 0 || m < 8)) return OperandPath::Elementwise;
+    if (b_k_major(t) ? (k & 7) != 0 : ((n & 7) != 0 || n < 8)) return OperandPath::Elementwise;
     const uint64_t a_elems = a_k_major(t) ? (uint64_t)m * lda : (uint64_t)k * lda;
     const uint64_t b_elems = b_k_major(t) ? (uint64_t)n * ldb : (uint64_t)k * ldb;
-    if (a_elems >= (1ull << 30) || b_elems >= (1ull << 30)) return false;
-    if (a_k_major(t) ? (k & 7) != 0 : ((m & 7) != 0 || m < 8)) return false;
-    if (b_k_major(t) ? (k & 7) != 0 : ((n & 7) != 0 || n < 8)) return false;
-    return true;
+    if (a_elems < (1ull << 30) && b_elems < (1ull << 30)) return OperandPath::Fast;
+    if (lda < (a_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd) && ldb < (b_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd))
+        return OperandPath::Wide;
+    return OperandPath::Elementwise;
 }
 
-static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, bool aligned, uint32_t m, uint32_t n,
-                     uint32_t k, uint32_t split_req, GemmPlan *p) {
+static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, OperandPath path, uint32_t m,
+                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p) {
+    const bool aligned = path != OperandPath::Elementwise, wide = path == OperandPath::Wide;
     bool stream_k = split_req == T0G_STREAM_K;
     if (stream_k) split_req = 1;
     if (!aligned && tile->bm == 256) tile = &kTiles[1];   // no element-wise-load variant of the 256x256 tile
-    if (tile->bm != 256 || k == 0) stream_k = false;      // the data-parallel kernel then
+    if (wide) tile = &kTiles[0];                           // the wide kernels are 256x256 only
+    if (tile->bm != 256 || k == 0 || wide) stream_k = false;   // the data-parallel kernel then
     p->stream_k = stream_k;
     p->sk_ipt = stream_k ? (k + kTileK - 1) / kTileK : 0;
     p->tile = tile;
@@ -237,14 +253,14 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, boo
     // variant (the CU's LDS then holds one workgroup with 128 KB of stages;
     // measured 10 % faster on 256x256x32768 split 16, while 128x128 gained
     // nothing on 128x4096x4096 split 8 and keeps its 4-stage ring).
-    const bool deep = aligned && tile->bm == 64 && (uint64_t)p->tiles_m * p->tiles_n * sk <= kNumCUs;
+    const bool deep = aligned && !wide && tile->bm == 64 && (uint64_t)p->tiles_m * p->tiles_n * sk <= kNumCUs;
     // The 256x256 kernels with a K-contiguous A (NN, NT) run 8 waves in
     // ping-pong; with an M-contiguous A (TN, TT) every fragment is a transposed
     // LDS read and the 4-wave kernel, with half the fragment reads per CU, is
     // faster.
     p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
-                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (deep ? "_d" : "") : "_u") +
+                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (wide ? "_x" : deep ? "_d" : "") : "_u") +
                 (stream_k ? "_sk" : "");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
@@ -253,10 +269,12 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, boo
     return T0G_OK;
 }
 
-// Per-thread operand offsets inside the kernels are 32-bit element counts.
+// The element-wise kernels (operands the fast path cannot take) use 32-bit
+// element offsets.
 static int check_extent(const char *what, uint64_t rows, uint64_t ld) {
     if (rows * ld >= (1ull << 31))
-        return fail(T0G_ERR_INVALID_ARG, "%s spans %llu elements; the gfx950 kernels address < 2^31", what,
+        return fail(T0G_ERR_INVALID_ARG,
+                    "%s spans %llu elements; unaligned operands (taken element-wise) must stay below 2^31", what,
                     (unsigned long long)(rows * ld));
     return T0G_OK;
 }
@@ -428,16 +446,18 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
     cfg->transpose = t;
     cfg->epilogue = d->epi_chain ? (uint32_t)T0G_EPI_STORE_F32 : d->epilogue;
     if ((rc = validate(cfg))) return rc;
-    if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
-    if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
     const uint32_t sk = d->split_k ? d->split_k : cfg_split(cfg);
     if (sk == T0G_STREAM_K && (cfg->tile_m != 256 || cfg->tile_n != 256))
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the 256x256 tile");
     if (sk > kMaxSplitK && sk != T0G_STREAM_K)
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u > %u", sk, kMaxSplitK);
     const TileDef *tile = find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
-    const bool aligned = operands_aligned(d->a, d->b, d->m, d->n, d->k, o->lda, o->ldb, t);
-    return make_plan(tile, t, d->out_dtype == T0G_BF16, aligned, d->m, d->n, d->k, sk, plan);
+    const OperandPath path = operand_path(d->a, d->b, d->m, d->n, d->k, o->lda, o->ldb, t);
+    if (path == OperandPath::Elementwise) {
+        if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
+        if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
+    }
+    return make_plan(tile, t, d->out_dtype == T0G_BF16, path, d->m, d->n, d->k, sk, plan);
 }
 
 }  // namespace t0g
@@ -785,15 +805,19 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
         o.c_split_stride = y_split_stride;
     }
     int rc;
-    if ((rc = check_extent("X", o.m, o.lda))) return rc;
-    if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
     const TileDef *tile = find_tile(cfg.tile_m, cfg.tile_n, cfg.tile_k, cfg.wg_size);
-    const bool aligned = operands_aligned(o.a, o.b, o.m, o.n, o.k, o.lda, o.ldb, cfg.transpose);
+    const OperandPath path = operand_path(o.a, o.b, o.m, o.n, o.k, o.lda, o.ldb, cfg.transpose);
+    if (path == OperandPath::Elementwise) {
+        if ((rc = check_extent("X", o.m, o.lda))) return rc;
+        if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
+    }
     GemmPlan p;
-    if ((rc = make_plan(tile, cfg.transpose, false, aligned, o.m, o.n, o.k, sk, &p))) return rc;
-    if (p.tile != tile)   // the element-wise variant has a different tile: honour the caller's grid instead
-        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "tile %ux%u needs 16-byte aligned rows (K %% 8 == 0)", cfg.tile_m,
-                    cfg.tile_n);
+    if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p))) return rc;
+    if (p.tile != tile)   // another tile than the caller's grid was built for: refuse rather than re-grid
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG,
+                    "tile %ux%u cannot take these operands (rows must be 16-byte aligned with K %% 8 == 0; "
+                    "operands of 2^30 elements or more need the 256x256 tile)",
+                    cfg.tile_m, cfg.tile_n);
     p.tiles_m = tiles_m;
     p.tiles_n = tiles_n;
     p.splits = sk;

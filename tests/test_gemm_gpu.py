@@ -717,25 +717,42 @@ def test_linear_regression_training_reduces_loss(rt, bufs):
 
 
 # ---- the largest operands ---------------------------------------------------
+BIG_K, BIG_ROWS = 16384, 131080   # 131080 x 16384 = 2^31 + 2^17 bf16 values: 4.3 GB
+
+
 @pytest.fixture(scope="module")
 def big_a():
-    """2^30 random bf16 values (2 GiB): A of up to 65536 x 16384 (or 16384 x 65536)."""
-    return o.rand_bf16_xorshift(1 << 30, 99)
+    """BIG_ROWS * BIG_K random bf16 values (just over 2^31 elements)."""
+    return o.rand_bf16_xorshift(BIG_ROWS * BIG_K, 99)
 
 
-@pytest.mark.parametrize("layout,m,path", [("NT", 65528, "fast"), ("NT", 65536, "generic"),
-                                           ("TN", 65528, "fast"), ("TN", 65536, "generic")])
-def test_largest_operands(rt, bufs, big_a, layout, m, path):
-    """A just below 2^30 elements runs on the fast kernels with offsets reaching 2 GiB;
-    exactly 2^30 goes to the element-wise kernels; both checked on oracle rows taken up
-    to the last row (K-contiguous A for NT, M-contiguous A for TN)."""
-    k, n = 16384, 256
-    _log(f"[case] largest operands {layout} {m}x{n}x{k} ({path})")
+@pytest.mark.parametrize("layout,m", [("NT", 65528), ("NT", 65536), ("NT", BIG_ROWS), ("TN", 65536),
+                                      ("TN", BIG_ROWS)])
+def test_largest_operands(rt, bufs, big_a, layout, m):
+    """A of 1 to 4.3 GB (up to 2^31 + 2^17 elements): the fast kernels just below 2^30
+    elements, the wide 256x256 kernels from there (descriptors rebased per tile for the
+    K-contiguous A of NT, per K stage for the M-contiguous A of TN); oracle rows taken up
+    to the last row."""
+    k, n = BIG_K, 256
+    _log(f"[case] largest operands {layout} {m}x{n}x{k}")
     a_st = big_a[: m * k]
     b_st = o.rand_bf16_xorshift(n * k, 7)
-    desc = t0g.gemm_desc(0, 0, 0, m, n, k, transpose=layout)
-    assert t0g.gemm_kernel_name(desc).endswith("_u") == (path == "generic")
+    name = t0g.gemm_kernel_name(t0g.gemm_desc(1 << 12, 1 << 12, 0, m, n, k, transpose=layout))
+    assert name.endswith("_x") == (m * k >= 1 << 30), name
     c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k)
     rows = np.array([0, 1, 255, 256, m // 2 + 3, m - 257, m - 2, m - 1])
     ref = o.gemm_rows(layout, a_st, b_st, m, n, k, rows)
     check_parity(c[rows], ref, k, f"largest {layout} {m}x{n}x{k}")
+
+
+def test_largest_n_contiguous_b(rt, bufs, big_a):
+    """NN with B [K][N] of 4.3 GB (N = 131080): the M/N-contiguous operand past 2^31
+    elements; sampled rows cover every output column."""
+    m, n, k = 256, BIG_ROWS, BIG_K
+    _log(f"[case] largest B NN {m}x{n}x{k}")
+    a_st = o.rand_bf16_xorshift(m * k, 11)
+    b_st = big_a[: k * n]
+    c = run_gemm(rt, bufs, "NN", a_st, b_st, m, n, k)
+    rows = np.array([0, 77, 255])
+    ref = o.gemm_rows("NN", a_st, b_st, m, n, k, rows)
+    check_parity(c[rows], ref, k, f"largest B NN {m}x{n}x{k}")

@@ -214,19 +214,37 @@ def test_desc_chain_validation():
 
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 def test_operand_size_limits(layout):
-    """The fast kernels address each operand with 32-bit buffer offsets: operands below
-    2^30 elements take them, larger ones the element-wise kernel (32-bit element offsets),
-    and 2^31 elements or more are refused with an error instead of overflowing."""
+    """Operands below 2^30 elements take the fast kernels; larger aligned ones the wide
+    256x256 kernels (_x: descriptors rebased per tile or K stage), whatever the config
+    asked for, as long as the leading dimension stays below 2^22 (K-contiguous) or
+    2^24 - 256 (M/N-contiguous) elements; the rest goes element-wise (_u, 32-bit element
+    offsets), where 2^31 elements or more are refused with an error."""
     k, n = 16384, 256
     a, b = 1 << 12, 1 << 40   # 16-byte aligned device addresses (not dereferenced here)
 
-    def name(m):
-        return t0g.gemm_kernel_name(t0g.gemm_desc(a, b, 0, m, n, k, transpose=layout, out_dtype=t0g.BF16))
+    def name(m, a=a, k=k, **kw):
+        return t0g.gemm_kernel_name(t0g.gemm_desc(a, b, 0, m, n, k, transpose=layout, out_dtype=t0g.BF16, **kw))
 
     below = (1 << 30) // k - 8   # a multiple of 8: M-contiguous rows stay 16-byte aligned
-    assert name(below).startswith("t0g_gemm_256x256_k64_") and not name(below).endswith("_u")   # below 2^30
-    assert name((1 << 30) // k).endswith("_u")                                    # exactly 2^30
-    assert name((1 << 31) // k - 1).endswith("_u")
+    assert name(below) == f"t0g_gemm_256x256_k64_{layout.lower()}_bf16"
+    for m in ((1 << 30) // k, (1 << 31) // k, (1 << 34) // k):                    # 1 GiB .. 32 GiB of A
+        assert name(m) == f"t0g_gemm_256x256_k64_{layout.lower()}_bf16_x", m
+    c128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    assert name((1 << 31) // k, config=c128).endswith("_bf16_x")                   # forced onto 256x256
+    assert name((1 << 31) // k, config=c128.copy(split_k=2)) == f"t0g_gemm_256x256_k64_{layout.lower()}_f32_x"
+    sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+    assert name((1 << 31) // k, config=sk).endswith("_bf16_x")                     # no wide stream-K kernel
+    # unaligned A: element-wise, refused once A spans 2^31 elements
+    assert name((1 << 31) // k - 8, a=a + 2).endswith("_u")
     with pytest.raises(t0g.T0gError) as e:
-        name((1 << 31) // k)                                                      # 2^31 elements
+        name((1 << 31) // k, a=a + 2)
+    assert e.value.code == t0g.ERR_INVALID_ARG
+    # leading dimensions past the wide kernels' offset range: element-wise
+    a_k = layout in ("NT", "NN")
+    big_ld = (1 << 22) if a_k else (1 << 24)
+    m = 1 << 12 if a_k else big_ld - 512      # A of about 2^34 (K-contiguous) or 2^31 (M/N-contiguous) elements
+    kk = k if a_k else 128
+    assert name(m, k=kk, lda=big_ld - 512).endswith("_x")
+    with pytest.raises(t0g.T0gError) as e:    # past the bound: element-wise, which cannot take 2^31 elements
+        name(m, k=kk, lda=big_ld)
     assert e.value.code == t0g.ERR_INVALID_ARG
