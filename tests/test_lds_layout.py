@@ -324,3 +324,51 @@ def test_mfma16_kernel_mnmajor_fragments(waves, wtn):
             for kk in range(2):
                 for stage in (0, 65536):
                     assert frag16_mnmajor_kernel(lds, wcol, sub, kk, stage) == expected16(wcol, sub, kk)
+
+
+# ---- wide kernels (_x): descriptor offsets stay below 2 GiB -------------------
+# The host sends an aligned operand of 2^30 elements or more to the _x kernels when
+# its leading dimension is below 2^22 (K-contiguous) or 2^24 - 256 (M/N-contiguous)
+# elements (test_host_api.py::test_operand_size_limits).  Their descriptors start
+# at the tile's first row (K-contiguous) or the stage's first k row (M/N-contiguous)
+# and span at most 2 GiB, with 0x80000000 reserved as the out-of-range offset: every
+# 16-byte piece a lane fetches must end at or below 2^31 bytes from that start, and
+# rebasing must not move any piece.
+KMAJOR_LD_BOUND, MNMAJOR_LD_BOUND = 1 << 22, (1 << 24) - 256
+
+
+@pytest.mark.parametrize("waves", [4, 8])
+def test_wide_kmajor_offsets(waves):
+    ld = KMAJOR_LD_BOUND - 8                      # largest allowed (rows stay 16-byte aligned)
+    step = 16 * waves * ld                        # bytes between a wave's DMA instructions
+    worst = 0
+    for wave in range(waves):
+        for lane in range(64):
+            r0 = 8 * wave + (lane >> 3)
+            c = (lane & 7) ^ fk(r0, 64)
+            off0 = (r0 * ld + c * 8) * 2          # from the tile's first row
+            for i in range(256 * 128 // 1024 // waves):
+                off = off0 + i * step
+                worst = max(worst, off + 16)
+                for row0, k0 in ((0, 0), (256 * 12345, 64 * 7)):     # rebasing moves nothing
+                    rowb = row0 * ld * 2
+                    assert rowb + k0 * 2 + off == ((row0 + r0 + 8 * waves * i) * ld + k0 + c * 8) * 2
+    assert worst <= 1 << 31
+
+
+@pytest.mark.parametrize("waves", [4, 8])
+def test_wide_mnmajor_offsets(waves):
+    ld = MNMAJOR_LD_BOUND - 8
+    row0 = (ld - 1) // 256 * 256                  # the last tile of a row, ending up to 255 past it
+    step = 4 * waves * ld
+    worst = 0
+    for wave in range(waves):
+        for lane in range(64):
+            k0, slot = 2 * wave + (lane >> 5), lane & 31
+            for i in range(64 * 512 // 1024 // waves):
+                k = k0 + 2 * waves * i
+                lg = (slot >> 1) ^ fm16(k, 16)
+                off = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2   # from the stage's first k row
+                assert off == (k0 * ld + row0 + lg * 16 + (slot & 1) * 8) * 2 + i * step
+                worst = max(worst, off + 16)
+    assert worst <= 1 << 31
