@@ -243,11 +243,14 @@ def test_c4b_split_k(rt, bufs, split_k):
 
 @pytest.mark.parametrize("m,n,k,sk,out", [(256, 256, 32768, 16, t0g.F32), (256, 256, 32768, 16, t0g.BF16),
                                            (100, 66, 2048, 8, t0g.F32), (100, 66, 2048, 8, t0g.BF16),
-                                           (128, 4096, 4096, 8, t0g.BF16)])
+                                           (128, 4096, 4096, 8, t0g.BF16), (512, 4096, 2048, 4, t0g.F32),
+                                           (512, 4096, 2048, 6, t0g.BF16)])
 def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
     """The on-device reduce equals the reference's host loop (plane order, from
     0.0, fp32) applied to the same partial planes, bit for bit; N % 4 != 0
-    takes the element-wise reduce, the others the 4-wide one."""
+    takes the element-wise reduce, outputs of 2^21 elements or more the 8-wide
+    one (with a split count that is not a multiple of its 4 planes in flight),
+    the others the 4-wide one."""
     _log(f"[case] reduce order {m}x{n}x{k} sk={sk} out={out}")
     a_mk = o.rand_bf16_lcg(m * k, 5 + m).reshape(m, k)
     b_nk = o.rand_bf16_lcg(n * k, 9 + n).reshape(n, k)
@@ -546,10 +549,11 @@ def test_epilogue_chains(rt, bufs, chain, preset, layout, m, n, k):
     assert np.array_equal(c16, o.f32_to_bf16_rne(c32)), "bf16 output is not RNE of the f32 output"
 
 
-@pytest.mark.parametrize("split_k", [4, 16])
-def test_epilogue_chain_after_split_k_reduce(rt, bufs, split_k):
-    """With split-K the chain runs once, in the plane-ordered reduce."""
-    m, n, k = 256, 320, 4096
+@pytest.mark.parametrize("split_k,m,n", [(4, 256, 320), (16, 256, 320), (4, 512, 4096)])
+def test_epilogue_chain_after_split_k_reduce(rt, bufs, split_k, m, n):
+    """With split-K the chain runs once, in the plane-ordered reduce (4-wide, and
+    8-wide for the 512 x 4096 output)."""
+    k = 4096
     chain = ("bias", "gelu", "scale", "clamp")
     a, b, a_st, b_st, bias = _chain_case(m, n, k, "NT", 21)
     ref = o.epilogue_chain(o.gemm("NT", a, b, m, n, k), chain, bias=bias, scale=2.0, clamp=(-1.0, 3.0))
