@@ -68,10 +68,12 @@ MLP_SHAPES = [("NN", 1024, 11008, 4096), ("NN", 1024, 4096, 11008), ("NT", 1024,
               ("NT", 1024, 4096, 11008), ("TN", 11008, 4096, 1024), ("TN", 4096, 11008, 1024)]
 
 
-def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None):
+def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False):
     """forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
     dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out.  configs: one
-    GemmConfig per GEMM (in MLP_SHAPES order) instead of auto_select's."""
+    GemmConfig per GEMM (in MLP_SHAPES order) instead of auto_select's.  grouped: the
+    GEMMs that do not depend on each other go through t0g_gemm_group: H, then
+    {Y, dH, dW2}, then {dX, dW1}."""
     bsz, d_in, d_hid = 1024, 4096, 11008
     g = torch.Generator(device="cuda").manual_seed(7)
     x = torch.randn((bsz, d_in), generator=g, device="cuda").to(torch.bfloat16)
@@ -94,16 +96,23 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None):
         t0g.gemm_desc(p(h), p(dy), p(dw2), d_hid, d_in, bsz, transpose="TN", out_dtype=t0g.BF16, config=cf[4]),
         t0g.gemm_desc(p(x), p(dh), p(dw1), d_in, d_hid, bsz, transpose="TN", out_dtype=t0g.BF16, config=cf[5]),
     ]
+    def step():
+        if grouped:
+            rt.gemm_desc(descs[0])
+            rt.gemm_group([descs[1], descs[2], descs[4]])
+            rt.gemm_group([descs[3], descs[5]])
+        else:
+            for d in descs:
+                rt.gemm_desc(d)
+
     for _ in range(warmup):
-        for d in descs:
-            rt.gemm_desc(d)
+        step()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(steps):
-        for d in descs:
-            rt.gemm_desc(d)
+        step()
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
@@ -417,6 +426,9 @@ def main():
         log("[bench] MLP step")
         extra["mlp_step_1024x4096x11008"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
                                                      max(2, args.warmup // 10))
+        log("[bench] MLP step, independent GEMMs grouped")
+        extra["mlp_step_1024x4096x11008_grouped"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
+                                                             max(2, args.warmup // 10), grouped=True)
         log("[bench] GemmTuner on the BASELINE shapes")
         extra["tuner"] = tuner_extra(t0g, torch, rt, stream, max(10, args.steps // 2), max(10, args.warmup // 4))
         log("[bench] stream-K")

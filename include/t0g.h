@@ -276,6 +276,14 @@ typedef struct t0g_gemm_desc {
 /* Enqueue C = op(A) * op(B) (+ epilogue) on the device stream (asynchronous).
  * split_k > 1: fp32 partial planes, then a deterministic plane-ordered reduce. */
 T0G_API int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *desc);
+/* Enqueue n GEMMs that do not depend on each other (no output of one is an
+ * input or output of another) to run concurrently: round-robin over the device
+ * stream and two side streams forked from it (default priority, each with its
+ * own split-K workspace); work enqueued on the device stream afterwards runs
+ * after all of them.  Stream-K configs take the data-parallel schedule here.
+ * No reference counterpart: the reference's single AQL queue runs one kernel at
+ * a time (src/kfd/mod.rs:1313-1319). */
+T0G_API int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n);
 /* Bytes of workspace t0g_gemm would use for desc (0 without split-K). */
 T0G_API int t0g_gemm_workspace_size(const t0g_gemm_desc *desc, size_t *bytes);
 /* Name of the gfx950 kernel symbol t0g_gemm would launch for desc. */

@@ -11,6 +11,7 @@
 #include <string.h>
 #include <time.h>
 
+#include <algorithm>
 #include <atomic>
 #include <memory>
 #include <mutex>
@@ -74,6 +75,14 @@ struct t0g_device {
     size_t conv_bytes = 0;
     uint32_t num_cus = 0;      // compute units: the stream-K grid
     uint64_t sk_sync = 0;      // stream-K control words and ready flags (zero between launches)
+    // t0g_gemm_group: side streams (default priority), each with its own split-K
+    // workspace, and the events that fork them from and join them back into `stream`
+    static constexpr int kSides = 2;
+    hipStream_t side[kSides] = {};
+    uint64_t side_ws[kSides] = {};
+    size_t side_ws_bytes[kSides] = {};
+    hipEvent_t fork_ev = nullptr;
+    hipEvent_t join_ev[kSides] = {};
 };
 
 namespace t0g {
@@ -546,6 +555,15 @@ int t0g_device_close(t0g_device *dev) {
     if (dev->ws) (void)hipFree((void *)dev->ws);
     if (dev->conv) (void)hipFree((void *)dev->conv);
     if (dev->sk_sync) (void)hipFree((void *)dev->sk_sync);
+    for (int i = 0; i < t0g_device::kSides; ++i) {
+        if (dev->side[i]) {
+            if (!dev->poisoned) (void)hipStreamSynchronize(dev->side[i]);
+            (void)hipStreamDestroy(dev->side[i]);
+        }
+        if (dev->side_ws[i]) (void)hipFree((void *)dev->side_ws[i]);
+        if (dev->join_ev[i]) (void)hipEventDestroy(dev->join_ev[i]);
+    }
+    if (dev->fork_ev) (void)hipEventDestroy(dev->fork_ev);
     for (uint64_t a : dev->allocations) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
@@ -933,6 +951,86 @@ int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
     if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
     std::lock_guard<std::mutex> lk(dev->mu);
     return gemm_locked(dev, d);
+}
+
+// Independent GEMMs, round-robin over the device stream and the side streams.
+// Stream-K keeps one control block per device, so grouped GEMMs take the
+// data-parallel schedule instead (stream-K launches must not overlap).
+int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    if (n && !descs) return fail(T0G_ERR_INVALID_ARG, "descs is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if (n <= 1) return n ? gemm_locked(dev, descs) : ok();
+    const int sides = (int)std::min<uint32_t>(n - 1, t0g_device::kSides);
+    hipError_t e;
+    for (int i = 0; i < sides; ++i) {
+        if (!dev->side[i] && (e = T0G_HIP(hipStreamCreateWithFlags(&dev->side[i], hipStreamNonBlocking))) != hipSuccess) {
+            dev->side[i] = nullptr;
+            return hip_fail(e, "hipStreamCreate(side stream)");
+        }
+        if (!dev->join_ev[i] &&
+            (e = T0G_HIP(hipEventCreateWithFlags(&dev->join_ev[i], hipEventDisableTiming))) != hipSuccess) {
+            dev->join_ev[i] = nullptr;
+            return hip_fail(e, "hipEventCreate(join)");
+        }
+    }
+    if (!dev->fork_ev && (e = T0G_HIP(hipEventCreateWithFlags(&dev->fork_ev, hipEventDisableTiming))) != hipSuccess) {
+        dev->fork_ev = nullptr;
+        return hip_fail(e, "hipEventCreate(fork)");
+    }
+    // validate every descriptor before anything is enqueued
+    for (uint32_t i = 0; i < n; ++i) {
+        t0g_gemm_config cfg;
+        GemmPlan p;
+        GemmOperands o;
+        if ((rc = resolve_desc(&descs[i], &cfg, &p, &o))) return fail(rc, "descs[%u]: %s", i, g_last_error.c_str());
+    }
+    if ((e = T0G_HIP(hipEventRecord(dev->fork_ev, dev->stream))) != hipSuccess)
+        return poison(dev, hip_fail(e, "hipEventRecord(fork)"));
+    for (int i = 0; i < sides; ++i)
+        if ((e = T0G_HIP(hipStreamWaitEvent(dev->side[i], dev->fork_ev, 0))) != hipSuccess)
+            return poison(dev, hip_fail(e, "hipStreamWaitEvent(fork)"));
+    const hipStream_t main_stream = dev->stream;
+    const uint64_t main_ws = dev->ws;
+    const size_t main_ws_bytes = dev->ws_bytes;
+    int first_rc = T0G_OK;
+    for (uint32_t i = 0; i < n && !first_rc; ++i) {
+        t0g_gemm_desc d = descs[i];
+        t0g_gemm_config cfg;
+        GemmPlan p;
+        GemmOperands o;
+        (void)resolve_desc(&d, &cfg, &p, &o);
+        t0g_gemm_config dp_cfg;
+        if (p.stream_k) {   // the same tile, data-parallel
+            dp_cfg = cfg;
+            dp_cfg.split_k = 0;
+            d.config = &dp_cfg;
+            d.split_k = 1;
+        }
+        const int s = (int)(i % (uint32_t)(sides + 1)) - 1;   // -1: the device stream
+        if (s >= 0) {
+            dev->stream = dev->side[s];
+            dev->ws = dev->side_ws[s];
+            dev->ws_bytes = dev->side_ws_bytes[s];
+        }
+        first_rc = gemm_locked(dev, &d);
+        if (s >= 0) {
+            dev->side_ws[s] = dev->ws;
+            dev->side_ws_bytes[s] = dev->ws_bytes;
+            dev->stream = main_stream;
+            dev->ws = main_ws;
+            dev->ws_bytes = main_ws_bytes;
+        }
+    }
+    // join whatever was enqueued, also after a failure
+    for (int i = 0; i < sides; ++i) {
+        if ((e = T0G_HIP(hipEventRecord(dev->join_ev[i], dev->side[i]))) != hipSuccess ||
+            (e = T0G_HIP(hipStreamWaitEvent(dev->stream, dev->join_ev[i], 0))) != hipSuccess)
+            return poison(dev, hip_fail(e, "join of a side stream"));
+    }
+    return first_rc ? first_rc : ok();
 }
 
 }  // extern "C"

@@ -200,6 +200,7 @@ _sig("t0g_dispatch_async", ctypes.c_int, _p, _p, _u32p, _p, ctypes.c_size_t)
 _sig("t0g_wait_idle", ctypes.c_int, _p)
 _sig("t0g_gemm", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
 _sig("t0g_gemm_workspace_size", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_size_t))
+_sig("t0g_gemm_group", ctypes.c_int, _p, ctypes.POINTER(GemmDesc), _u32)
 _sig("t0g_gemm_kernel_name", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_size_t)
 _sig("t0g_f32_to_bf16", ctypes.c_int, _p, _u64, _u64, ctypes.c_size_t)
 _sig("t0g_matmul_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
@@ -559,6 +560,11 @@ class GpuRuntime:
 
     def gemm_desc(self, desc):
         _check(_lib.t0g_gemm(self.handle, ctypes.byref(desc)))
+
+    def gemm_group(self, descs):
+        """Enqueue independent GEMMs (GemmDesc list) to run concurrently."""
+        arr = (GemmDesc * max(1, len(descs)))(*descs)
+        _check(_lib.t0g_gemm_group(self.handle, arr, len(descs)))
 
     def gemm(self, a, b, c, m, n, k, **kw):
         """Enqueue C = op(A) op(B) on the device stream (asynchronous)."""

@@ -760,3 +760,67 @@ def test_largest_n_contiguous_b(rt, bufs, big_a):
     rows = np.array([0, 77, 255])
     ref = o.gemm_rows("NN", a_st, b_st, m, n, k, rows)
     check_parity(c[rows], ref, k, f"largest B NN {m}x{n}x{k}")
+
+
+# ---- independent GEMMs run concurrently (t0g_gemm_group) ----------------------
+def test_gemm_group_equals_one_by_one(rt, bufs):
+    """Five independent GEMMs of different families (split-K with its reduce, fused
+    epilogue, bf16 and f32 outputs, a stream-K config, which a group runs data-parallel)
+    enqueued as one group over the device stream and two side streams: every output
+    equals the same GEMM run alone, bit for bit, twice in a row; then work on the
+    device stream sees all of them finished."""
+    p256 = t0g.GemmConfig.preset("tile_256x256_k64")
+    sk = p256.copy(split_k=t0g.STREAM_K)
+    cases = [  # (layout, m, n, k, out, extra desc fields, config used alone)
+        ("NN", 1024, 4096, 11008, t0g.BF16, {}, None),                          # split 4 + reduce
+        ("NT", 128, 4096, 4096, t0g.BF16, {}, None),                            # 128x128 split 8
+        ("TN", 512, 768, 1000, t0g.F32, {"epilogue_ops": ["bias", "silu"]}, None),
+        ("NN", 4352, 4096, 1024, t0g.BF16, {"config": sk}, p256),               # stream-K asked for
+        ("TT", 300, 264, 1024, t0g.F32, {}, None),                              # element-wise rows
+    ]
+    bias = bufs.up(np.linspace(-1, 1, 768, dtype=np.float32))
+    descs, singles, outs = [], [], []
+    for i, (lay, m, n, k, out, extra, alone_cfg) in enumerate(cases):
+        a_mk = o.rand_bf16_lcg(m * k, 31 + i).reshape(m, k)
+        b_nk = o.rand_bf16_lcg(n * k, 41 + i).reshape(n, k)
+        a_st, b_st = stored_operands(lay, a_mk, b_nk)
+        a, b = bufs.up(a_st), bufs.up(b_st)
+        esz = 4 if out == t0g.F32 else 2
+        c_grp, c_one = bufs.alloc(m * n * esz, fill=0xFF), bufs.alloc(m * n * esz, fill=0)
+        kw = dict(transpose=lay, out_dtype=out, **extra)
+        if "epilogue_ops" in extra:
+            kw["bias"] = bias
+        descs.append(t0g.gemm_desc(a, b, c_grp, m, n, k, **kw))
+        if alone_cfg is not None:
+            kw["config"] = alone_cfg
+        singles.append(t0g.gemm_desc(a, b, c_one, m, n, k, **kw))
+        outs.append((c_grp, c_one, (m, n), np.float32 if out == t0g.F32 else np.uint16, m * n * esz))
+    for d in singles:
+        rt.gemm_desc(d)
+    rt.wait_idle()
+    for _ in range(2):
+        for c_grp, _, _, _, nbytes in outs:
+            rt.memset(c_grp, 0xFF, nbytes)
+        rt.gemm_group(descs)
+        rt.wait_idle()
+        for c_grp, c_one, shape, dt, _ in outs:
+            assert np.array_equal(rt.read(c_grp, shape, dt), rt.read(c_one, shape, dt))
+
+
+def test_gemm_group_edge_cases(rt, bufs):
+    m = n = k = 256
+    a = bufs.up(o.rand_bf16_lcg(m * k, 1))
+    b = bufs.up(o.rand_bf16_lcg(n * k, 2))
+    c = bufs.alloc(m * n * 4, fill=0)
+    rt.gemm_group([])                                                   # nothing to do
+    rt.gemm_group([t0g.gemm_desc(a, b, c, m, n, k)])                    # one GEMM: the device stream
+    rt.wait_idle()
+    check_parity(rt.read(c, (m, n), np.float32),
+                 o.gemm("NT", o.rand_bf16_lcg(m * k, 1), o.rand_bf16_lcg(n * k, 2), m, n, k), k, "group of one")
+    bad = t0g.gemm_desc(a, b, c, m, n, k, transpose=9)
+    rt.memset(c, 0, m * n * 4)
+    with pytest.raises(t0g.T0gError) as e:                              # refused before anything runs
+        rt.gemm_group([t0g.gemm_desc(a, b, c, m, n, k), bad])
+    assert e.value.code == t0g.ERR_INVALID_ARG and "descs[1]" in str(e.value)
+    rt.wait_idle()
+    assert not rt.read(c, (m, n), np.float32).any()
