@@ -20,8 +20,8 @@
 //     reference leaves to the caller (src/t0/test_tile_gemm_suite.rs:62-99);
 //   * split-K slices write fp32 planes at c + split * c_split_stride; the
 //     deterministic plane-ordered reduction is t0g_splitk_reduce_*;
-//   * block ids are remapped so each XCD (own L2) works on a contiguous,
-//     M-grouped patch of output tiles.
+//   * workgroup ids are remapped so each XCD (own L2) works on a contiguous
+//     range of (K slice, M-grouped output tile) pairs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -306,10 +306,35 @@ __device__ __forceinline__ void apply_epilogue_n(float (&v)[N], const float (&bv
     }
 }
 
+// Output tile index and K slice of this workgroup (grid x is exactly the tile
+// count, grid y the split count).  The dispatcher deals workgroups out to the
+// 8 XCDs round-robin in linear order (x fastest).  With XCD_REMAP the linear id
+// is permuted so that XCD c owns the contiguous range [c*total/8, (c+1)*total/8)
+// of slice-major (split, tile) order: the workgroups of one K slice share an
+// L2, which then fetches each A and B panel of that slice once instead of once
+// per XCD.  Without split-K this is the plain tile remap.  (The 256x256
+// kernels keep the tile-only remap: measured, the extra prologue work cost
+// their 4096^3 launch 1-1.5 %, more than the split-K shapes on that tile gain.)
+struct GridPos {
+    uint32_t tile, split;
+};
+__device__ __forceinline__ GridPos grid_pos(const T0gGemmArgs& p) {
+    const uint32_t nblk = p.tiles_m * p.tiles_n;
+    uint32_t tile = blockIdx.x, split = blockIdx.y;
+    const uint64_t total = (uint64_t)nblk * gridDim.y;
+    if ((p.flags & T0G_FLAG_XCD_REMAP) && (total & 7u) == 0 && total <= 0xFFFFFFFFull) {
+        const uint32_t lin = split * nblk + tile;
+        const uint32_t l = (lin & 7u) * (uint32_t)(total >> 3) + (lin >> 3);
+        split = l / nblk;
+        tile = l - split * nblk;
+    }
+    return GridPos{tile, split};
+}
+
 template <int SM, int SN, bool OUT_BF16>
 __device__ __forceinline__ void store_tile(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
-                                           uint32_t col0, uint32_t l32, uint32_t g) {
-    const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+                                           uint32_t col0, uint32_t l32, uint32_t g, uint32_t split) {
+    const uint64_t cbase = p.c + (uint64_t)split * p.c_split_stride;
     float bv[SN];
     load_bias_cols<SN>(p, col0, l32, bv);
 #pragma unroll
@@ -349,7 +374,7 @@ struct VecEpilogue {
 
 template <int SM, int SN, bool OUT_BF16>
 __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
-                                               uint32_t col0, uint32_t lane, uint32_t lds, bool vec) {
+                                               uint32_t col0, uint32_t lane, uint32_t lds, bool vec, uint32_t split) {
     typedef VecEpilogue<SN> E;
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) float lds_f32;
@@ -371,7 +396,7 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
             bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + cl + c) * 4u, 0, 0));
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     }
-    const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
+    const uint64_t cbase = p.c + (uint64_t)split * p.c_split_stride;
     const uint32_t esize = OUT_BF16 ? 2u : 4u;
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
@@ -446,9 +471,8 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
     const uint32_t tid = threadIdx.x;
 
     // --- output tile of this workgroup ----------------------------------------
-    uint32_t bid = blockIdx.x;
-    const uint32_t nblk = p.tiles_m * p.tiles_n;   // grid x is exactly the tile count
-    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    const GridPos gp = grid_pos(p);
+    const uint32_t bid = gp.tile;
     const uint32_t gm = p.group_m;
     const uint32_t per_group = gm * p.tiles_n;
     const uint32_t group = bid / per_group;
@@ -458,7 +482,7 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
     const uint32_t m0 = (first_m + in_group % gsz) * BM;
     const uint32_t n0 = (in_group / gsz) * BN;
 
-    const uint32_t kbeg = blockIdx.y * p.k_per_split;
+    const uint32_t kbeg = gp.split * p.k_per_split;
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
     const int nkt = kend > kbeg ? (int)((kend - kbeg + kTileK - 1) / kTileK) : 0;
 
@@ -526,7 +550,7 @@ __device__ __forceinline__ void gemm_tile(const T0gGemmArgs& p) {
         }
     }
 
-    store_tile<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l32, g);
+    store_tile<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l32, g, gp.split);
 }
 
 // ---------------------------------------------------------------------------
@@ -959,9 +983,8 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
     const uint32_t tid = threadIdx.x;
-    uint32_t bid = blockIdx.x;
-    const uint32_t nblk = p.tiles_m * p.tiles_n;
-    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    const GridPos gp = grid_pos(p);
+    const uint32_t bid = gp.tile;
     const uint32_t gm = p.group_m;
     const uint32_t per_group = gm * p.tiles_n;
     const uint32_t group = bid / per_group;
@@ -971,7 +994,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     const uint32_t m0 = (first_m + in_group % gsz) * BM;
     const uint32_t n0 = (in_group / gsz) * BN;
 
-    const uint32_t kbeg = blockIdx.y * p.k_per_split;
+    const uint32_t kbeg = gp.split * p.k_per_split;
     const uint32_t kend = min(p.k, kbeg + p.k_per_split);
     const int nst = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
 
@@ -1011,7 +1034,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     barrier_no_fence();   // and every wave is done with the ring
     const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
     store_tile_vec<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                     lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec);
+                                     lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec, gp.split);
 }
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the

@@ -93,7 +93,7 @@ typedef struct T0gConvertArgs {
     uint32_t flags;          /* T0G_CONVERT_VEC                                   */
 } T0gConvertArgs;
 
-#define T0G_FLAG_XCD_REMAP 1u   /* remap block ids so each XCD owns a contiguous tile range */
+#define T0G_FLAG_XCD_REMAP 1u   /* remap workgroup ids so each XCD owns a contiguous tile (128x128, 64x64: (split, tile)) range */
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
 #define T0G_FLAG_BIAS 4u        /* the chain reads bias[col]                                     */
 #define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
