@@ -276,6 +276,46 @@ def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
     check_parity(host, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"reduce order {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("preset", ["tile_64x64_k64", "tile_128x128_k64"])
+@pytest.mark.parametrize("tiles_m,tiles_n,sk,layout", [(1, 1, 8, "NT"), (2, 2, 2, "NN"), (1, 3, 8, "TN"),
+                                                       (2, 3, 4, "NT"), (4, 4, 16, "NN"), (1, 5, 8, "NT"),
+                                                       (3, 2, 4, "TT"), (2, 4, 3, "NT")])
+def test_split_k_grid_remap_covers_every_slice(rt, bufs, preset, tiles_m, tiles_n, sk, layout):
+    """Split-K grids of 8k workgroups on the 128x128 and 64x64 tiles are permuted
+    slice-major over the XCDs; every (tile, K slice) pair must still be computed
+    exactly once.  The partial planes start as NaN (0xFF bytes), so a pair the
+    permutation skipped would leave NaN in its plane; each plane is checked
+    against the oracle's product over that slice, and the reduced output
+    against the whole product (ragged N edge included)."""
+    tile = 64 if "64x64" in preset else 128
+    m, n, k = tiles_m * tile, tiles_n * tile - 8, sk * 128
+    _log(f"[case] split remap {preset} {tiles_m}x{tiles_n} tiles sk={sk} {layout}")
+    a_mk = o.rand_bf16_lcg(m * k, 17 + m + sk).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 19 + n + sk).reshape(n, k)
+    a = bufs.up(a_mk if layout[0] == "N" else np.ascontiguousarray(a_mk.T))
+    b = bufs.up(b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T))
+    c = bufs.alloc(m * n * 4, fill=0)
+    cfg = t0g.GemmConfig.preset(preset)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk)
+    need = t0g.gemm_workspace_size(d)
+    ws = bufs.alloc(need, fill=0xFF)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk,
+                      workspace=ws, workspace_bytes=need)
+    assert f"{tile}x{tile}" in t0g.gemm_kernel_name(d)
+    rt.gemm_desc(d)
+    rt.wait_idle()
+    planes = rt.read(ws, (sk, m, n), np.float32)
+    assert not np.isnan(planes).any(), "a (tile, K slice) pair was not computed"
+    kps = k // sk
+    for s in range(sk):
+        part = o.gemm("NT", np.ascontiguousarray(a_mk[:, s * kps:(s + 1) * kps]),
+                      np.ascontiguousarray(b_nk[:, s * kps:(s + 1) * kps]), m, n, kps)
+        check_parity(planes[s], part, kps, f"plane {s}")
+    got = rt.read(c, (m, n), np.float32)
+    assert np.array_equal(got.view(np.uint32), o.splitk_reduce(planes).view(np.uint32))
+    check_parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"split remap {tiles_m}x{tiles_n} sk={sk}")
+
+
 def _randn_pair(m, n, k, seed_a=2, seed_b=3):
     a = o.randn_bf16(m * k, seed_a, 0.02)
     b = o.randn_bf16(k * n, seed_b, 0.02)
