@@ -36,6 +36,22 @@ def make_inputs(torch, m, n, k, layout, seed):
     return a, b
 
 
+def _warm(torch, launch, count, min_ms=200.0):
+    """`count` untimed launches, then more until at least min_ms of load has run: the
+    shader clock of a power-limited MI355X keeps rising for ~0.2 s under load (4096^3
+    NN: 101.6 us per launch after 20 ms of warm-up, 99.8 us after 0.2 s and after 1 s),
+    so a line timed earlier reads a few percent below the steady state a training loop
+    runs at.  The timed region is still exactly the requested launches."""
+    t0 = time.perf_counter()
+    for _ in range(count):
+        launch()
+    torch.cuda.synchronize()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(8):
+            launch()
+        torch.cuda.synchronize()
+
+
 def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, out=None, epilogue_ops=None,
               config=None):
     a, b = make_inputs(torch, m, n, k, layout, seed)
@@ -44,9 +60,7 @@ def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, ou
     desc = t0g.gemm_desc(a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, transpose=layout, out_dtype=t0g.BF16,
                          epilogue_ops=epilogue_ops, bias=bias.data_ptr() if epilogue_ops else 0, config=config)
     kname = t0g.gemm_kernel_name(desc)
-    for _ in range(warmup):
-        rt.gemm_desc(desc)
-    torch.cuda.synchronize()
+    _warm(torch, lambda: rt.gemm_desc(desc), warmup)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t_start = time.perf_counter()
@@ -105,9 +119,7 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False)
             for d in descs:
                 rt.gemm_desc(d)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _warm(torch, step, warmup)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -123,9 +135,7 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False)
 
 
 def _event_ms(torch, stream, fn, steps, warmup):
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    _warm(torch, fn, warmup)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -291,7 +301,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200,
-                    help="untimed launches first; the shader clock needs ~20 ms of load to settle")
+                    help="untimed launches first (each line also warms for at least 0.2 s of load, the "
+                         "time the shader clock takes to reach its steady state)")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",

@@ -383,37 +383,58 @@ int tune_locked(t0g_tuner *t, t0g_device *dev, const TuneKey &key, const TuneEnt
         rc = t0g_memcpy_h2d(dev, a, host.data(), a_elems * 2);
         if (!rc) rc = t0g_memcpy_h2d(dev, b, host.data() + (host.size() - b_elems), b_elems * 2);
     }
-    std::vector<std::pair<t0g_gemm_config, double>> results;
+    // Every candidate is timed in kRounds interleaved rounds (the middle one in
+    // reverse order) and ranked by the median of all its samples: the shader clock
+    // of a power-limited MI355X drifts with temperature over a tuning run, and one
+    // block of samples per candidate let that drift decide near ties.  The first
+    // round warms each candidate for about 10 ms (by the model's time), the clock's
+    // settling time under load; later rounds for a quarter of that.
+    constexpr int kRounds = 3;
+    std::vector<std::vector<double>> samples(cands.size());
+    std::vector<char> failed(cands.size(), 0);
     std::string last_failure;
     const double flop = 2.0 * key.m * key.n * key.k;
-    for (size_t i = 0; !rc && i < cands.size(); ++i) {
-        t0g_gemm_desc d;
-        memset(&d, 0, sizeof d);
-        d.a = a;
-        d.b = b;
-        d.c = c;
-        d.m = key.m;
-        d.n = key.n;
-        d.k = key.k;
-        d.transpose = key.transpose;
-        d.out_dtype = key.out_dtype;
-        d.config = &cands[i];
-        // Warm-up of about 10 ms per candidate (by the model's time): the shader
-        // clock of a power-limited MI355X needs that long under load to settle,
-        // and a ranking taken at an unsettled clock favours whoever runs later.
-        const TileDef *tile = find_tile(cands[i].tile_m, cands[i].tile_n, cands[i].tile_k, cands[i].wg_size);
-        const double model_us = cands[i].split_k == T0G_STREAM_K ? model_time_sk_us(key.m, key.k, key.n)
-                                : tile ? model_time_us(*tile, key.m, key.k, key.n, cfg_split(&cands[i]))
-                                       : 100.0;
-        const uint32_t warm = (uint32_t)std::min(500.0, std::max(2.0, 10000.0 / std::max(model_us, 1.0)));
-        std::vector<double> ms;
-        int brc = time_gemm(dev, &d, warm, t->n_iters, &ms);
-        if (brc) {
-            last_failure = config_name(cands[i]) + ": " + g_last_error;
-            int poisoned = 0;
-            if (t0g_device_is_poisoned(dev, &poisoned) == T0G_OK && poisoned) break;
-            continue;
+    bool poisoned_dev = false;
+    for (int r = 0; !rc && !poisoned_dev && r < kRounds; ++r) {
+        for (size_t j = 0; j < cands.size(); ++j) {
+            const size_t i = (r == 1) ? cands.size() - 1 - j : j;
+            if (failed[i]) continue;
+            t0g_gemm_desc d;
+            memset(&d, 0, sizeof d);
+            d.a = a;
+            d.b = b;
+            d.c = c;
+            d.m = key.m;
+            d.n = key.n;
+            d.k = key.k;
+            d.transpose = key.transpose;
+            d.out_dtype = key.out_dtype;
+            d.config = &cands[i];
+            const TileDef *tile = find_tile(cands[i].tile_m, cands[i].tile_n, cands[i].tile_k, cands[i].wg_size);
+            const double model_us = cands[i].split_k == T0G_STREAM_K ? model_time_sk_us(key.m, key.k, key.n)
+                                    : tile ? model_time_us(*tile, key.m, key.k, key.n, cfg_split(&cands[i]))
+                                           : 100.0;
+            const double warm_us = r == 0 ? 10000.0 : 2500.0;
+            const uint32_t warm = (uint32_t)std::min(500.0, std::max(2.0, warm_us / std::max(model_us, 1.0)));
+            std::vector<double> ms;
+            int brc = time_gemm(dev, &d, warm, t->n_iters, &ms);
+            if (brc) {
+                last_failure = config_name(cands[i]) + ": " + g_last_error;
+                failed[i] = 1;
+                int poisoned = 0;
+                if (t0g_device_is_poisoned(dev, &poisoned) == T0G_OK && poisoned) {
+                    poisoned_dev = true;
+                    break;
+                }
+                continue;
+            }
+            samples[i].insert(samples[i].end(), ms.begin(), ms.end());
         }
+    }
+    std::vector<std::pair<t0g_gemm_config, double>> results;
+    for (size_t i = 0; i < cands.size(); ++i) {
+        if (failed[i] || samples[i].empty()) continue;
+        std::vector<double> &ms = samples[i];
         std::sort(ms.begin(), ms.end());
         const double med = ms[ms.size() / 2];
         results.emplace_back(cands[i], med > 0 ? flop / (med * 1e-3) / 1e12 : 0.0);
