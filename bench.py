@@ -2,10 +2,10 @@
 """bf16 GEMM throughput on one MI355X through libt0g's C ABI.
 
 One step = one C = A*B GEMM (bf16 in, fp32 accumulate, bf16 out, row-major NN)
-at BASELINE configs[1], M = N = K = 4096, inputs N(0,1)*0.02 resident in HBM.
+at configs[1] of BASELINE.json, M = N = K = 4096, inputs N(0,1)*0.02 resident in HBM.
 Prints ONE JSON line.  Besides `value` (TFLOPS of the timed steps) the line
 carries the dominant kernel's roofline (HIP events on the stream the kernels
-run on), the other BASELINE configs under "extra", and the CPU oracle timed on
+run on), the other benchmark configurations under "extra", and the CPU oracle timed on
 this host under "cpu_baseline".
 """
 import argparse
@@ -83,7 +83,7 @@ MLP_SHAPES = [("NN", 1024, 11008, 4096), ("NN", 1024, 4096, 11008), ("NT", 1024,
 
 
 def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False):
-    """forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
+    """Benchmark config 5: forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
     dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out.  configs: one
     GemmConfig per GEMM (in MLP_SHAPES order) instead of auto_select's.  grouped: the
     GEMMs that do not depend on each other go through t0g_gemm_group: H, then
@@ -176,7 +176,7 @@ def ignis_linear(torch, rt, stream, steps, warmup):
 
 
 def tuner_extra(t0g, torch, rt, stream, steps, warmup):
-    """GemmTuner (src/t0/auto_gemm.rs) on the BASELINE shapes, from an empty cache: the
+    """GemmTuner (src/t0/auto_gemm.rs) on the benchmark shapes, from an empty cache: the
     tuning time, a cache hit's time, and each shape's GEMM with auto_select's config
     and with the tuned one (same harness as the other lines); then the MLP step with
     the tuned configs."""
@@ -303,7 +303,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200,
                     help="untimed launches first (each line also warms for at least 0.2 s of load, the "
                          "time the shader clock takes to reach its steady state)")
-    ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other benchmark configurations")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
                     help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
@@ -440,7 +440,7 @@ def main():
         log("[bench] MLP step, independent GEMMs grouped")
         extra["mlp_step_1024x4096x11008_grouped"] = mlp_step(t0g, torch, rt, stream, max(3, args.steps // 5),
                                                              max(2, args.warmup // 10), grouped=True)
-        log("[bench] GemmTuner on the BASELINE shapes")
+        log("[bench] GemmTuner on the benchmark shapes")
         extra["tuner"] = tuner_extra(t0g, torch, rt, stream, max(10, args.steps // 2), max(10, args.warmup // 4))
         log("[bench] stream-K")
         extra["stream_k"] = stream_k_extra(t0g, torch, rt, stream, max(10, args.steps // 4), max(10, args.warmup // 8))

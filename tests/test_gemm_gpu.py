@@ -1,6 +1,6 @@
 """Parity of the gfx950 GEMM kernels with the CPU oracle, through the C ABI.
 
-Gate, on the fp32 result: relF <= 5e-3 and
+Gate (the parity bar of the benchmark), on the fp32 result: relF <= 5e-3 and
 max|d| <= 1e-2 * sqrt(K/256).  bf16 output is checked bit-exactly against
 round-to-nearest-even of the same kernel's fp32 result.  Inputs come from the
 reference's own generators (restated in the oracle) with its seeds.
@@ -95,7 +95,7 @@ PRESETS = ["tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 @pytest.mark.parametrize("preset", PRESETS + [None])
 def test_c1_256_cubed_all_layouts(rt, bufs, layout, preset):
-    """256^3, U(-1,1) xorshift data with the seeds of
+    """Benchmark config 1: 256^3, U(-1,1) xorshift data with the seeds of
     examples/test_gemm_correctness.rs:128-129; fp32 and bf16 output."""
     m = n = k = 256
     _log(f"[case] c1 layout={layout} preset={preset}")
@@ -214,7 +214,7 @@ def test_k_zero_gives_zero_plus_bias(rt, bufs):
 
 
 def test_c4a_thin(rt, bufs):
-    """BASELINE config 4a: M=128, K=4096, N=4096, LCG data (tile_boundary_tests.rs:42-49)."""
+    """Benchmark config 4a: M=128, K=4096, N=4096, LCG data (tile_boundary_tests.rs:42-49)."""
     m, k, n = 128, 4096, 4096
     a_mk = o.rand_bf16_lcg(m * k, 42 + m).reshape(m, k)
     b_nk = o.rand_bf16_lcg(n * k, 137 + n).reshape(n, k)
@@ -227,7 +227,7 @@ def test_c4a_thin(rt, bufs):
 
 @pytest.mark.parametrize("split_k", [0, 8, 16, 32, 64])
 def test_c4b_split_k(rt, bufs, split_k):
-    """BASELINE config 4b: M=N=256, K=32768, fp32 partial planes reduced in plane order."""
+    """Benchmark config 4b: M=N=256, K=32768, fp32 partial planes reduced in plane order."""
     m, k, n = 256, 32768, 256
     _log(f"[case] split-K sk={split_k}")
     a_mk = o.rand_bf16_lcg(m * k, 42 + m).reshape(m, k)
@@ -333,7 +333,7 @@ def _sample_rows(m):
 
 @pytest.mark.parametrize("layout", ["NN", "NT"])
 def test_c2_4096_cubed(rt, bufs, layout):
-    """4096^3, N(0,1)*0.02.  Sampled rows against the oracle,
+    """Benchmark config 2: 4096^3, N(0,1)*0.02.  Sampled rows against the oracle,
     whole-matrix bf16 == RNE(fp32)."""
     m = n = k = 4096
     _log(f"[case] 4096^3 {layout}")
@@ -347,7 +347,7 @@ def test_c2_4096_cubed(rt, bufs, layout):
 
 
 def test_c3_8192_cubed(rt, bufs):
-    """8192^3 NN, N(0,1)*0.02, sampled rows + bf16 consistency."""
+    """Benchmark config 3: 8192^3 NN, N(0,1)*0.02, sampled rows + bf16 consistency."""
     m = n = k = 8192
     _log("[case] 8192^3 NN")
     a, b = _randn_pair(m, n, k, 4, 5)
@@ -360,7 +360,7 @@ def test_c3_8192_cubed(rt, bufs):
 
 
 def test_c5_mlp_step(rt, bufs):
-    """2-layer MLP step, batch 1024, 4096 -> 11008 -> 4096.
+    """Benchmark config 5: 2-layer MLP step, batch 1024, 4096 -> 11008 -> 4096.
     He-init weights (src/ignis/nn/linear.rs:36-43, [in, out] layout, RNE to bf16
     as src/ignis/ops/bf16_matmul.rs:357-384 does).  Forward H = X W1, Y = H W2 (NN);
     backward dH = dY W2^T, dX = dH W1^T (NT on the stored weights), dW2 = H^T dY,

@@ -105,7 +105,7 @@ def test_stream_k_plan(layout):
     (4352, 4096, 8192, True), (4352, 4096, 4096, True), (8448, 8192, 8192, True),
     # fuller last rounds stay data-parallel (measured: 144 tiles a tie, 576 tiles slower)
     (4608, 4608, 8192, False), (3072, 3072, 8192, False), (6144, 6144, 6144, False),
-    # BASELINE shapes keep their schedules (measured slower with stream-K: MLP 97 vs 88 us)
+    # The benchmark shapes keep their schedules (measured slower with stream-K: MLP 97 vs 88 us)
     (4096, 4096, 4096, False), (8192, 8192, 8192, False), (128, 4096, 4096, False), (256, 256, 32768, False),
     (1024, 11008, 4096, False), (1024, 4096, 11008, False), (11008, 4096, 1024, False), (256, 256, 256, False)])
 def test_auto_select_takes_stream_k_only_with_a_margin(m, n, k, sk):
