@@ -36,7 +36,10 @@ def make_inputs(torch, m, n, k, layout, seed):
     return a, b
 
 
-def _warm(torch, launch, count, min_ms=200.0):
+WARM_MIN_MS = 200.0
+
+
+def _warm(torch, launch, count, min_ms=WARM_MIN_MS):
     """`count` untimed launches, then more until at least min_ms of load has run: the
     shader clock of a power-limited MI355X keeps rising for ~0.2 s under load (4096^3
     NN: 101.6 us per launch after 20 ms of warm-up, 99.8 us after 0.2 s and after 1 s),
@@ -389,6 +392,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_load_s": WARM_MIN_MS / 1e3,   # each line also warms until this much load has run
         "ms_per_step": round(main_res["wall_ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
