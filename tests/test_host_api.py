@@ -163,6 +163,17 @@ def test_no_device_on_this_host_is_an_error():
     assert e.value.code == t0g.ERR_NO_DEVICE
 
 
+def test_gemm_group_argument_checks():
+    """t0g_gemm_group rejects a NULL device before touching the GPU, with or without
+    descriptors."""
+    lib = t0g._lib
+    d = t0g.gemm_desc(1, 2, 3, 64, 64, 64)
+    arr = (t0g.GemmDesc * 1)(d)
+    assert lib.t0g_gemm_group(None, arr, 1) == t0g.ERR_INVALID_ARG
+    assert "device" in lib.t0g_last_error().decode()
+    assert lib.t0g_gemm_group(None, None, 0) == t0g.ERR_INVALID_ARG
+
+
 def test_injected_hip_failure_maps_to_error():
     t0g.debug_fail_hip_call(1)
     try:
