@@ -360,8 +360,9 @@ T0G_API int t0g_tuner_cache_dir(t0g_tuner *tuner, char *buf, size_t len);
 T0G_API int t0g_tune_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t max,
                                 t0g_gemm_config *out, uint32_t *count);
 /* GemmTuner::tune(rt, m, n, k) (auto_gemm.rs:82-163): memory, then disk, then
- * benchmark (random bf16 operands, device time by HIP events, median of n_iters
- * after ~10 ms of warm-up launches per candidate) and persist.  Synchronous. */
+ * benchmark (random bf16 operands, device time by HIP events; the candidates
+ * timed in three interleaved rounds of n_iters launches, each after warm-up
+ * launches, and ranked by the median of their samples) and persist.  Synchronous. */
 T0G_API int t0g_tuner_tune(t0g_tuner *tuner, t0g_device *dev, uint32_t m, uint32_t n, uint32_t k,
                            uint32_t transpose, uint32_t out_dtype, t0g_gemm_config *best);
 /* Cached result without benchmarking: *found = 0 on a miss. */
