@@ -1101,7 +1101,8 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
     if (p.flags & T0G_REDUCE_VEC) {
         const uint32_t nq = p.n >> 2;
         const uint32_t total = p.m * nq;
-        for (uint32_t q = blockIdx.x * 256 + threadIdx.x; q < total; q += p.grid_blocks * 256) {
+        // blockDim.x: 256, or 64 for outputs too small to give every CU a 256-thread block
+        for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += p.grid_blocks * blockDim.x) {
             const uint32_t row = q / nq, col = (q - row * nq) * 4;
             const uint64_t w = (uint64_t)row * p.ldw + col;
             f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};

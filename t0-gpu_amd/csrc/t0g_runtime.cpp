@@ -417,10 +417,13 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     if (vec8) r.flags |= T0G_REDUCE_VEC8;
     if (vec) r.flags |= T0G_REDUCE_VEC;
     const uint64_t total = vec8 ? (uint64_t)o.m * (o.n / 8) : vec ? (uint64_t)o.m * (o.n / 4) : (uint64_t)o.m * o.n;
-    uint64_t blocks = (total + 255) / 256;
+    // 4-wide outputs of fewer than 256 full blocks run 64-thread blocks, so every CU
+    // shares the plane reads (256 x 256: 64 CUs -> 256)
+    const uint32_t threads = (vec && total < 256u * 256u) ? 64u : 256u;
+    uint64_t blocks = (total + threads - 1) / threads;
     if (blocks > 4096) blocks = 4096;
     r.grid_blocks = (uint32_t)blocks;
-    return launch(dev, fr, (uint32_t)blocks, 1, 1, 256, &r, sizeof r);
+    return launch(dev, fr, (uint32_t)blocks, 1, 1, threads, &r, sizeof r);
 }
 
 static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *plan, GemmOperands *o) {
