@@ -1,0 +1,99 @@
+"""Seeded sweep of random GEMM problems through t0g_gemm against the CPU oracle.
+
+Each case draws a layout (NT/NN/TN/TT), M, N and K, a config (auto_select's or one of
+the three tiles), a split-K count, padded leading dimensions (some of them not a
+multiple of 8, which routes the operands to the element-wise kernels) and the
+output type.  Checked per case: parity of the fp32 result with the oracle
+(relF <= 5e-3, max|d| <= 1e-2 sqrt(K/256)), a second run equal bit for bit, and
+for bf16 output, equality with RNE of the same config's fp32 output.  The padding
+columns hold random values, so a kernel that reads past the logical operand
+breaks parity."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as o
+import t0g
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 48
+PRESETS = [None, "tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def rt():
+    r = t0g.GpuRuntime.new(0)
+    yield r
+    r.close()
+
+
+def _case(i):
+    rng = np.random.default_rng(1000 + i)
+    layout = ["NT", "NN", "TN", "TT"][i % 4]
+    m = int(rng.integers(1, 701))
+    n = int(rng.integers(1, 701))
+    k = int(rng.integers(1, 1201))
+    preset = PRESETS[int(rng.integers(0, len(PRESETS)))]
+    splits = [s for s in (1, 2, 3, 4, 8) if s == 1 or k >= s * 64]
+    split = 0 if preset is None else int(rng.choice(splits))
+    pads = [int(rng.choice([0, 0, 8, 13])) for _ in range(3)]
+    out = t0g.BF16 if rng.integers(0, 2) else t0g.F32
+    return rng, layout, m, n, k, preset, split, pads, out
+
+
+def _stored(logical, pad, rng):
+    """logical [rows][cols] bf16 bits in a [rows][cols + pad] array whose padding holds random bf16."""
+    rows, cols = logical.shape
+    full = o.rand_bf16_lcg(rows * (cols + pad), int(rng.integers(1, 1 << 30))).reshape(rows, cols + pad)
+    full[:, :cols] = logical
+    return np.ascontiguousarray(full)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_problem(rt, i):
+    rng, layout, m, n, k, preset, split, pads, out = _case(i)
+    _log(f"[case] sweep {i}: {layout} {m}x{n}x{k} preset={preset} split={split} pads={pads} "
+         f"out={'bf16' if out == t0g.BF16 else 'f32'}")
+    a_mk = o.rand_bf16_lcg(m * k, 7 * i + 1).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 7 * i + 2).reshape(n, k)
+    a_log = a_mk if layout in ("NT", "NN") else np.ascontiguousarray(a_mk.T)
+    b_log = b_nk if layout in ("NT", "TT") else np.ascontiguousarray(b_nk.T)
+    a_st = _stored(a_log, pads[0], rng)
+    b_st = _stored(b_log, pads[1], rng)
+    lda, ldb, ldc = a_st.shape[1], b_st.shape[1], n + pads[2]
+    kw = dict(transpose=layout, lda=lda, ldb=ldb, ldc=ldc, split_k=split)
+    if preset is not None:
+        kw["config"] = t0g.GemmConfig.preset(preset)
+    da, db = rt.upload(a_st), rt.upload(b_st)
+    dc = rt.alloc(m * ldc * 4)
+    dc2 = rt.alloc(m * ldc * 4)
+    try:
+        desc = t0g.gemm_desc(da, db, dc, m, n, k, out_dtype=t0g.F32, **kw)
+        _log(f"[kernel] {t0g.gemm_kernel_name(desc)}")
+        rt.memset(dc, 0xFF, m * ldc * 4)
+        rt.gemm(da, db, dc, m, n, k, out_dtype=t0g.F32, **kw)
+        rt.memset(dc2, 0, m * ldc * 4)
+        rt.gemm(da, db, dc2, m, n, k, out_dtype=t0g.F32, **kw)
+        rt.wait_idle()
+        c = rt.read(dc, (m, ldc), np.float32)[:, :n]
+        c2 = rt.read(dc2, (m, ldc), np.float32)[:, :n]
+        assert np.array_equal(c.view(np.uint32), c2.view(np.uint32)), "two runs differ"
+        ok, relf, maxabs, bound = o.parity(c, o.gemm("NT", a_mk, b_nk, m, n, k), k)
+        _log(f"[parity] sweep {i}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
+        assert ok, f"relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
+        if out == t0g.BF16:
+            rt.memset(dc2, 0xFF, m * ldc * 2)
+            rt.gemm(da, db, dc2, m, n, k, out_dtype=t0g.BF16, **kw)
+            rt.wait_idle()
+            c16 = rt.read(dc2, (m, ldc), np.uint16)[:, :n]
+            assert np.array_equal(c16, o.f32_to_bf16_rne(c)), "bf16 output is not RNE of the fp32 output"
+    finally:
+        for x in (da, db, dc, dc2):
+            rt.free(x)
