@@ -3,7 +3,9 @@
 Each case draws a layout (NT/NN/TN/TT), M, N and K, a config (auto_select's or one of
 the three tiles), a split-K count, padded leading dimensions (some of them not a
 multiple of 8, which routes the operands to the element-wise kernels) and the
-output type.  Checked per case: parity of the fp32 result with the oracle
+output type; every third case also an epilogue chain of one to four ops with
+random bias, scale and clamp bounds (checked against the oracle's restatement of
+the chain).  Checked per case: parity of the fp32 result with the oracle
 (relF <= 5e-3, max|d| <= 1e-2 sqrt(K/256)), a second run equal bit for bit, and
 for bf16 output, equality with RNE of the same config's fp32 output.  The padding
 columns hold random values, so a kernel that reads past the logical operand
@@ -45,7 +47,11 @@ def _case(i):
     split = 0 if preset is None else int(rng.choice(splits))
     pads = [int(rng.choice([0, 0, 8, 13])) for _ in range(3)]
     out = t0g.BF16 if rng.integers(0, 2) else t0g.F32
-    return rng, layout, m, n, k, preset, split, pads, out
+    chain = None
+    if i % 3 == 2:
+        names = ["bias", "scale", "relu", "silu", "gelu", "abs", "neg", "clamp"]
+        chain = [names[int(x)] for x in rng.integers(0, len(names), int(rng.integers(1, 5)))]
+    return rng, layout, m, n, k, preset, split, pads, out, chain
 
 
 def _stored(logical, pad, rng):
@@ -58,9 +64,9 @@ def _stored(logical, pad, rng):
 
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_problem(rt, i):
-    rng, layout, m, n, k, preset, split, pads, out = _case(i)
+    rng, layout, m, n, k, preset, split, pads, out, chain = _case(i)
     _log(f"[case] sweep {i}: {layout} {m}x{n}x{k} preset={preset} split={split} pads={pads} "
-         f"out={'bf16' if out == t0g.BF16 else 'f32'}")
+         f"out={'bf16' if out == t0g.BF16 else 'f32'} chain={chain}")
     a_mk = o.rand_bf16_lcg(m * k, 7 * i + 1).reshape(m, k)
     b_nk = o.rand_bf16_lcg(n * k, 7 * i + 2).reshape(n, k)
     a_log = a_mk if layout in ("NT", "NN") else np.ascontiguousarray(a_mk.T)
@@ -71,9 +77,18 @@ def test_random_problem(rt, i):
     kw = dict(transpose=layout, lda=lda, ldb=ldb, ldc=ldc, split_k=split)
     if preset is not None:
         kw["config"] = t0g.GemmConfig.preset(preset)
+    bias = None
+    if chain:
+        bias = (rng.standard_normal(n) * 0.05).astype(np.float32)
+        scale = float(rng.uniform(-2.0, 2.0))
+        lo = float(rng.uniform(-0.1, 0.0))
+        kw.update(epilogue_ops=chain, epi_scale=scale, clamp=(lo, lo + float(rng.uniform(0.01, 0.2))))
     da, db = rt.upload(a_st), rt.upload(b_st)
     dc = rt.alloc(m * ldc * 4)
     dc2 = rt.alloc(m * ldc * 4)
+    dbias = rt.upload(bias) if bias is not None else 0
+    if bias is not None:
+        kw["bias"] = dbias
     try:
         desc = t0g.gemm_desc(da, db, dc, m, n, k, out_dtype=t0g.F32, **kw)
         _log(f"[kernel] {t0g.gemm_kernel_name(desc)}")
@@ -85,7 +100,10 @@ def test_random_problem(rt, i):
         c = rt.read(dc, (m, ldc), np.float32)[:, :n]
         c2 = rt.read(dc2, (m, ldc), np.float32)[:, :n]
         assert np.array_equal(c.view(np.uint32), c2.view(np.uint32)), "two runs differ"
-        ok, relf, maxabs, bound = o.parity(c, o.gemm("NT", a_mk, b_nk, m, n, k), k)
+        ref = o.gemm("NT", a_mk, b_nk, m, n, k)
+        if chain:
+            ref = o.epilogue_chain(ref, chain, bias=bias, scale=kw["epi_scale"], clamp=kw["clamp"])
+        ok, relf, maxabs, bound = o.parity(c, ref, k)
         _log(f"[parity] sweep {i}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
         assert ok, f"relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
         if out == t0g.BF16:
@@ -95,5 +113,6 @@ def test_random_problem(rt, i):
             c16 = rt.read(dc2, (m, ldc), np.uint16)[:, :n]
             assert np.array_equal(c16, o.f32_to_bf16_rne(c)), "bf16 output is not RNE of the fp32 output"
     finally:
-        for x in (da, db, dc, dc2):
-            rt.free(x)
+        for x in (da, db, dc, dc2, dbias):
+            if x:
+                rt.free(x)
