@@ -75,7 +75,8 @@ def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, ou
     wall_s = time.perf_counter() - t_start
     ev_ms = e0.elapsed_time(e1)
     res = {"kernel": kname, "wall_ms_per_step": wall_s * 1e3 / steps, "event_ms_per_launch": ev_ms / steps,
-           "flop": 2.0 * m * n * k, "bytes_min": 2.0 * (m * k + k * n) + 2.0 * m * n}
+           "flop": 2.0 * m * n * k, "bytes_min": 2.0 * (m * k + k * n) + 2.0 * m * n, "desc": desc,
+           "tensors": (a, b, c, bias)}
     if out is not None:
         out["tensors"] = (a, b, c)
     return res
@@ -237,6 +238,109 @@ def stream_k_extra(t0g, torch, rt, stream, steps, warmup):
     return out
 
 
+def _amd_smi_sample():
+    """One reading of the GFX clocks (MHz, one per XCD) and the socket power (W) from
+    amd-smi, run as a child process (it reads the driver's metrics; it does not touch
+    this process's GPU context).  Returns (clocks, power, raw text) or None."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-g", "0", "-c", "-p", "--json"], capture_output=True,
+                             text=True, timeout=10)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    if out.returncode != 0:
+        return None
+    try:
+        js = json.loads(out.stdout)
+    except ValueError:
+        return None
+    clocks, power = [], []
+
+    def num(v):
+        if isinstance(v, dict):
+            v = v.get("value")
+        return float(v) if isinstance(v, (int, float)) else None
+
+    def walk(node, parent=""):
+        if isinstance(node, dict):
+            for key, val in node.items():
+                kl = str(key).lower()
+                if re.fullmatch(r"gfx_?\d*", kl) and isinstance(val, dict) and "clk" in val:
+                    v = num(val["clk"])
+                    if v is not None and v > 0:
+                        clocks.append(v)
+                elif kl in ("socket_power", "current_socket_power", "average_socket_power"):
+                    v = num(val)
+                    if v is not None and v > 0:
+                        power.append(v)
+                else:
+                    walk(val, kl)
+        elif isinstance(node, list):
+            for val in node:
+                walk(val, parent)
+
+    walk(js)
+    return clocks, (power[0] if power else None), out.stdout[:2000]
+
+
+def sustained_clock(torch, launch, seconds=2.0):
+    """Run `launch` back to back for `seconds` while a thread samples amd-smi; the
+    samples of the first 0.4 s (the clock's ramp under load) are dropped.  Returns the
+    median GFX clock over XCDs and samples, the median socket power, the sample count."""
+    import threading
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            s = _amd_smi_sample()
+            if s is None:
+                return
+            # readings under the 500 MHz DPM floor are deep-sleep samples of an idle XCD
+            clocks = [c for c in s[0] if c >= 500.0]
+            if time.perf_counter() - t0 > 0.4 and clocks:
+                samples.append((clocks, s[1], s[2]))
+            time.sleep(0.05)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(16):
+            launch()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    if not samples:
+        return None
+    clocks = sorted(c for s in samples for c in s[0])
+    powers = sorted(s[1] for s in samples if s[1] is not None)
+    return {"sclk_mhz_median": clocks[len(clocks) // 2], "sclk_mhz_min": clocks[0], "sclk_mhz_max": clocks[-1],
+            "socket_power_w_median": powers[len(powers) // 2] if powers else None, "samples": len(samples),
+            "source": "amd-smi metric -c -p (child process) while the GEMM ran back to back"}
+
+
+def clock_line(torch, rt, desc, flop, seconds=2.0):
+    """Measured shader clock next to a result, and the MFMA utilisation it implies: the
+    kernel's FLOP rate under the same sustained load over the dense bf16 rate at that
+    clock (256 CUs x 4096 FLOP per clock; every MFMA is useful work, checked with the
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 counter)."""
+    clk = sustained_clock(torch, lambda: rt.gemm_desc(desc), seconds)
+    if clk is None:
+        return {"sclk_mhz_median": None, "note": "amd-smi gave no clock reading on this host"}
+    return clk
+
+
+def _mfma_util(tflops, sclk_mhz):
+    """The FLOP rate over the dense bf16 rate at the measured clock (256 CUs x 4096
+    FLOP/clk): the fraction of cycles the MFMA pipes are busy with this GEMM."""
+    if not sclk_mhz:
+        return {"mfma_util": None}
+    at_clock = 256 * 4096 * sclk_mhz * 1e6 / 1e12
+    return {"dense_peak_at_sclk_tflops": round(at_clock, 1), "mfma_util": round(tflops / at_clock, 4)}
+
+
 def cold_gemm(t0g, torch, rt, stream, m, n, k, layout, trials):
     """One GEMM per trial after a 512 MB device copy that evicts the GEMM's operands from
     the 256 MB Infinity Cache and the L2s; each launch timed alone by HIP events; median."""
@@ -288,11 +392,20 @@ def cpu_baseline(torch, tensors, m, n, k, min_seconds):
     naive = 2.0 * rows * n * k / t_naive / 1e12
     cpu_model = None
     try:
-        with open("/proc/cpuinfo") as f:
-            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
-    except OSError:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        cpu_model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), None)
+    except (OSError, ValueError):
         pass
+    if not cpu_model:
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+        except OSError:
+            pass
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     return {"value": fast, "unit": "TFLOPS", "cores": threads, "kind": "port", "cpu_model": cpu_model,
+            "nproc": nproc, "host_cpus": os.cpu_count(),
             "sample": f"full {m}x{n}x{k} NN product x{reps} ({t_total:.1f} s, vectorised + OpenMP, "
                       f"bit-identical to the reference loop)",
             "naive_single_thread": {"value": naive, "unit": "TFLOPS", "cores": 1,
@@ -307,6 +420,7 @@ def main():
                     help="untimed launches first (each line also warms for at least 0.2 s of load, the "
                          "time the shader clock takes to reach its steady state)")
     ap.add_argument("--no-extra", action="store_true", help="skip the other benchmark configurations")
+    ap.add_argument("--no-clock", action="store_true", help="skip the shader-clock sampling (amd-smi) lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
                     help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
@@ -406,6 +520,10 @@ def main():
                      "frac": round(kern_tflops / PEAK_TFLOPS, 4), "traffic": traffic,
                      "per_launch_flop": main_res["flop"], "avg_launch_ms": round(main_res["event_ms_per_launch"], 5)},
     }
+    if not args.no_clock:
+        log("[bench] 4096^3 NN bf16: shader clock under sustained load")
+        line["clock"] = clock_line(torch, rt, main_res["desc"], main_res["flop"])
+        line["clock"].update(_mfma_util(kern_tflops, line["clock"].get("sclk_mhz_median")))
 
     if not args.no_extra:
         extra = {}
@@ -417,6 +535,12 @@ def main():
         t8 = r8["flop"] / (r8["event_ms_per_launch"] * 1e-3) / 1e12
         extra["gemm_nn_8192^3"] = {"tflops": round(t8, 2), "frac_of_peak": round(t8 / PEAK_TFLOPS, 4),
                                    "ms_per_launch": round(r8["event_ms_per_launch"], 4), "kernel": r8["kernel"]}
+        if not args.no_clock:
+            log("[bench] 8192^3 NN bf16: shader clock under sustained load")
+            ck8 = clock_line(torch, rt, r8["desc"], r8["flop"], seconds=3.0)
+            ck8.update(_mfma_util(t8, ck8.get("sclk_mhz_median")))
+            extra["gemm_nn_8192^3"]["clock"] = ck8
+        del r8
         log("[bench] 4096^3 NT bf16")
         rnt = time_gemm(t0g, torch, rt, stream, 4096, 4096, 4096, "NT", args.steps, args.warmup, seed=6)
         tnt = rnt["flop"] / (rnt["event_ms_per_launch"] * 1e-3) / 1e12

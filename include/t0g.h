@@ -125,11 +125,22 @@ T0G_API uint32_t t0g_config_n_waves(const t0g_gemm_config *cfg);
 T0G_API uint32_t t0g_config_lds_total(const t0g_gemm_config *cfg);
 /* GemmConfig::name (src/t0/gemm_gen.rs:207-227), same tag scheme. */
 T0G_API int t0g_config_name(const t0g_gemm_config *cfg, char *buf, size_t len);
+/* TileGemm::name (src/t0/tile_ir.rs:398-430): "tile_gemm_<m>x<n>_k<k>[_db][_skN][_mg][_wgp][_nn]"
+ * then the epilogue chain's "_op" tags (chain 0: cfg->epilogue's); TN/TT add
+ * "_tn"/"_tt" and stream-K "_streamk", which TileGemm has no name for. */
+T0G_API int t0g_tile_config_name(const t0g_gemm_config *cfg, uint32_t chain, char *buf, size_t len);
 
 /* auto_select(m, k, n) -> GemmConfig (src/t0/gemm_gen.rs:320-322): table
  * re-derived for 256 CUs (NT layout, f32 store epilogue). */
 T0G_API int t0g_auto_select(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
-/* tile_auto_select(m, k, n, transpose) (src/t0/tile_ir.rs:471-568). */
+/* tile_auto_select(m, k, n, transpose) (src/t0/tile_ir.rs:471-568): a config
+ * the tile ABI runs (t0g_tile_kernel_get + t0g_build_kernargs_m +
+ * t0g_tile_compute_grid + t0g_dispatch).  transpose is NT or NN (TileTranspose,
+ * src/t0/tile_ir.rs:73-78); the choice is the 256-CU model of t0g_auto_select
+ * without stream-K.  Split-K configs are runnable: with the y_split_stride of 0
+ * that build_kernargs_m writes, the library keeps the fp32 planes and reduces
+ * them into Y in plane order (the reference leaves them to the caller,
+ * src/t0/tile_ir.rs:3154-3157). */
 T0G_API int t0g_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose,
                                  t0g_gemm_config *out);
 
@@ -207,12 +218,39 @@ T0G_API int t0g_device_set_stream(t0g_device *dev, void *hip_stream);
 T0G_API int t0g_device_get_stream(t0g_device *dev, void **hip_stream);
 T0G_API int t0g_device_is_poisoned(t0g_device *dev, int *poisoned);
 
-/* KfdDevice::alloc_vram / GpuRuntime::{alloc, alloc_zero} (src/kfd/mod.rs:572,
- * src/ignis/gpu_context.rs:437-454).  Returns the device address. */
+/* GpuRuntime::{alloc, alloc_zero} over its BufferPool (src/ignis/gpu_context.rs:21-76,
+ * 437-446; KfdDevice::alloc_vram, src/kfd/mod.rs:572, when the pool has no buffer of
+ * the size).  Sizes are rounded up to whole 4 KiB pages; a recycled buffer of the
+ * same rounded size is reused, else hipMalloc.  Returns the device address. */
 T0G_API int t0g_alloc(t0g_device *dev, size_t bytes, uint64_t *addr);
 T0G_API int t0g_alloc_zero(t0g_device *dev, size_t bytes, uint64_t *addr);
-/* GpuBuffer drop (src/kfd/mod.rs:1057-1081); waits for the stream first. */
+/* GpuBuffer drop (src/kfd/mod.rs:1057-1081): hipFree, after waiting for the stream. */
 T0G_API int t0g_free(t0g_device *dev, uint64_t addr);
+/* GpuRuntime::recycle / BufferPool::recycle (src/ignis/gpu_context.rs:56-62, 457-459):
+ * return a live buffer to the pool instead of freeing it; no wait.  Work already
+ * queued on the device stream may still use it, so a later owner must use it in
+ * that stream's order (t0g_memcpy_*, t0g_gemm on the same stream are). */
+T0G_API int t0g_recycle(t0g_device *dev, uint64_t addr);
+/* BufferPool::clear (src/ignis/gpu_context.rs:65-69): free every recycled buffer
+ * (waits for the stream first). */
+T0G_API int t0g_pool_clear(t0g_device *dev);
+typedef struct t0g_pool_info {
+    uint64_t cached_bytes;     /* BufferPool::cached_bytes: recycled, not yet reused */
+    uint64_t cached_buffers;
+    uint64_t live_bytes;       /* allocated and not freed or recycled */
+    uint64_t live_buffers;
+    uint64_t hits, misses;     /* allocations served from the pool / by hipMalloc */
+} t0g_pool_info;
+T0G_API int t0g_pool_stats(t0g_device *dev, t0g_pool_info *out);
+/* GpuRuntime::alloc_f32 (src/ignis/gpu_context.rs:449-454): n floats, padded to
+ * whole 512-byte blocks (at least one), zeroed in device-stream order. */
+T0G_API int t0g_alloc_f32(t0g_device *dev, size_t n, uint64_t *addr);
+/* GpuRuntime::{write_f32, read_f32} (src/ignis/gpu_context.rs:463-480): synchronous;
+ * the read waits for queued work first, as read_f32 waits for idle. */
+T0G_API int t0g_write_f32(t0g_device *dev, uint64_t addr, const float *src, size_t n);
+T0G_API int t0g_read_f32(t0g_device *dev, uint64_t addr, float *dst, size_t n);
+/* GpuRuntime::upload_f32 (src/ignis/gpu_context.rs:482-487): alloc_f32 + write_f32. */
+T0G_API int t0g_upload_f32(t0g_device *dev, const float *src, size_t n, uint64_t *addr);
 /* GpuBuffer::{write, read, zero} (src/kfd/mod.rs:1000-1055): synchronous. */
 T0G_API int t0g_memcpy_h2d(t0g_device *dev, uint64_t dst, const void *src, size_t bytes);
 T0G_API int t0g_memcpy_d2h(t0g_device *dev, void *dst, uint64_t src, size_t bytes);
@@ -231,11 +269,30 @@ T0G_API int t0g_tile_kernel_get(t0g_device *dev, const t0g_gemm_config *cfg, t0g
  * cfg->epilogue must be T0G_EPI_STORE_F32 (the chain replaces it). */
 T0G_API int t0g_tile_kernel_get_epilogue(t0g_device *dev, const t0g_gemm_config *cfg, uint32_t chain,
                                          t0g_kernel **out);
+/* A kernel's entry in a gfx950 code object's AMDGPU metadata note, read on the
+ * host (no GPU needed).  The reference knows these from the kernel it generated
+ * (T0Kernel::{kernarg_size, lds_size, wg_size}, src/t0/compile.rs:495-510). */
+typedef struct t0g_kernel_meta {
+    uint32_t kernarg_size;          /* bytes of the caller's argument block (explicit arguments) */
+    uint32_t kernarg_segment_size;  /* the whole segment, with the runtime's hidden arguments   */
+    uint32_t group_segment_size;    /* static LDS bytes                                          */
+    uint32_t private_segment_size;  /* scratch bytes per lane                                    */
+    uint32_t max_workgroup_size;    /* largest workgroup the kernel was built for                */
+    uint32_t wavefront_size;
+} t0g_kernel_meta;
+/* code_object: a bare gfx950 ELF or a clang offload bundle holding one (size
+ * bytes, read with bounds checks); objects for other GPUs are refused. */
+T0G_API int t0g_code_object_kernel_meta(const void *code_object, size_t size, const char *symbol,
+                                        t0g_kernel_meta *out);
+
 /* GpuKernel::load(&device, &elf, &KernelLoadConfig{workgroup_size, lds_size})
- * (src/kfd/mod.rs:2559-2651, 2655): any gfx950 code object, launched raw.  Its
- * dispatches pass the kernargs block through unchanged: kernargs_len must be the
- * kernel's argument segment size (for this library's GEMM kernels,
- * sizeof(T0gGemmArgs) = 104 bytes). */
+ * (src/kfd/mod.rs:2559-2651, 2655): any gfx950 code object, launched raw.  The
+ * kernel's argument size is read from the code object's metadata, and every
+ * dispatch of it must pass exactly that many kernarg bytes (T0G_ERR_INVALID_ARG
+ * otherwise, before anything reaches the GPU; this library's GEMM kernels take
+ * 104).  A workgroup larger than the kernel was built for is refused here.
+ * lds_size is the kernel's total LDS, as in KernelLoadConfig: the part beyond
+ * the kernel's static LDS is requested as dynamic LDS at launch. */
 T0G_API int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size,
                             const char *symbol, const uint32_t workgroup_size[3],
                             uint32_t lds_size, t0g_kernel **out);
@@ -288,6 +345,31 @@ T0G_API int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t
 T0G_API int t0g_gemm_workspace_size(const t0g_gemm_desc *desc, size_t *bytes);
 /* Name of the gfx950 kernel symbol t0g_gemm would launch for desc. */
 T0G_API int t0g_gemm_kernel_name(const t0g_gemm_desc *desc, char *buf, size_t len);
+
+/* T0Kernel::compile(Target) / compile_with_info (src/t0/compile.rs:1115-1187)
+ * plus build_kernargs and compute_grid, for callers that load and launch the
+ * kernel themselves (GpuKernel::load + dispatch, or t0g_kernel_load +
+ * t0g_dispatch): the kernels are precompiled, so "compiling" selects the
+ * symbol t0g_gemm would launch for desc and returns the library's gfx950 code
+ * object, the symbol's workgroup size and LDS, its argument block for desc's
+ * operands and the grid in threads.  Host only.  Split-K (desc->split_k > 1 or
+ * the config's) writes fp32 partial planes to C, plane s at
+ * c + s * M * ldc * 4 bytes, which the caller sums in plane order as the
+ * reference's callers do (examples/test_gemm_correctness.rs:190-207); this
+ * needs out_dtype F32.  A stream-K config is compiled as the same tile without
+ * the split (its launches need the device's flag words: t0g_gemm only). */
+typedef struct t0g_compiled_kernel {
+    const void *code_object;    /* gfx950 code object (clang offload bundle); static, owned by the library */
+    size_t code_object_size;
+    char name[96];              /* kernel symbol in it                        */
+    uint32_t workgroup_size;    /* threads per workgroup along x (y = z = 1)  */
+    uint32_t lds_size;          /* static LDS bytes                           */
+    uint32_t kernarg_size;      /* bytes of kernargs[] to pass                */
+    uint32_t grid[3];           /* grid in threads for desc's problem          */
+    uint32_t splits;            /* fp32 planes written to C (1: C itself)      */
+    uint8_t kernargs[160];      /* argument block for desc's problem           */
+} t0g_compiled_kernel;
+T0G_API int t0g_gemm_compile(const t0g_gemm_desc *desc, t0g_compiled_kernel *out);
 
 /* ---- Ignis bf16_matmul caller path on f32 device tensors ------------------- *
  * src/ignis/ops/bf16_matmul.rs converts its f32 operands to bf16 on the CPU,
@@ -381,6 +463,24 @@ T0G_API int t0g_tuner_invalidate(t0g_tuner *tuner, uint32_t m, uint32_t n, uint3
 T0G_API int t0g_tuner_clear(t0g_tuner *tuner);
 /* report (auto_gemm.rs:405-417) into buf; *needed = bytes including the NUL. */
 T0G_API int t0g_tuner_report(t0g_tuner *tuner, char *buf, size_t len, size_t *needed);
+/* tune_tile_ir(rt, m, n, k) -> TileIrTuneResult (src/t0/cost_model.rs:757-1013):
+ * the tile ABI's configs (NT, f32 out, data-parallel or split-K; tuner NULL =
+ * the global one), looked up in memory, then in <cache_dir>/tile_ir_MxNxK.json
+ * (tile_ir_cache_path / load_tile_ir_cache, cost_model.rs:1059-1074), else
+ * benchmarked as t0g_tuner_tune does and saved with save_tile_ir_cache's keys
+ * (tile_m, tile_n, tile_k, split_k, wgp, tflops, all; cost_model.rs:1076-1093)
+ * plus "arch":"gfx950", wg_size and the size.  A file without "arch":"gfx950"
+ * (the gfx1100 build's) is a miss.  out->best runs through
+ * t0g_tile_kernel_get; ranking names are TileGemm::name()s. */
+T0G_API int t0g_tune_tile_ir(t0g_tuner *tuner, t0g_device *dev, uint32_t m, uint32_t n, uint32_t k,
+                             t0g_tune_result *out);
+T0G_API int t0g_tile_ir_lookup(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, t0g_tune_result *out,
+                               int *found);
+T0G_API int t0g_tile_ir_ranking(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, uint32_t i, char *name,
+                                size_t name_len, double *tflops);
+/* save_tile_ir_cache of a result (NT, f32) and its ranking, also into memory. */
+T0G_API int t0g_tile_ir_store(t0g_tuner *tuner, const t0g_tune_result *result, const char *const *names,
+                              const double *tflops, uint32_t n_all);
 /* auto_gemm(rt, a, b, c, m, n, k) (auto_gemm.rs:445-480): tune (NT, f32 out,
  * tuner NULL = the global one), then enqueue C[M][N] = A[M][K] * B[N][K]^T with
  * the best config; *tflops (may be NULL) = the cached measurement. */
@@ -394,8 +494,18 @@ T0G_API int t0g_auto_gemm(t0g_tuner *tuner, t0g_device *dev, uint64_t a, uint64_
 T0G_API uint32_t t0g_stream_k_begin(uint32_t total, uint32_t grid, uint32_t w);
 T0G_API uint32_t t0g_stream_k_worker(uint32_t total, uint32_t grid, uint32_t it);
 /* Ready-flag waits of stream-K launches on dev that gave up (0 unless a
- * workgroup waited past its spin limit); waits for the device stream. */
+ * workgroup waited past its spin limit); waits for the device stream.  Any
+ * wait on a stream that ran a stream-K launch (t0g_wait_idle, t0g_dispatch,
+ * t0g_memcpy_*, ...) checks this count first and, if it is not 0, poisons the
+ * device and returns T0G_ERR_TIMEOUT: the GEMM's cut tiles miss partial sums. */
 T0G_API int t0g_stream_k_timeouts(t0g_device *dev, uint32_t *count);
+/* Polls of a stream-K ready flag before a workgroup gives up (default 2^20,
+ * about a tenth of a second); applies to launches made after the call. */
+T0G_API int t0g_set_stream_k_spin_limit(uint32_t polls);
+/* on != 0: later stream-K launches wait on a control word nothing sets, so
+ * every wait of a cut tile gives up at the spin limit and the kernels still
+ * exit (a host-forced timeout for testing the error path); 0 restores. */
+T0G_API int t0g_debug_stream_k_stall(int on);
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
  * real device fault. */

@@ -880,9 +880,11 @@ __device__ __forceinline__ void gemm_tile_sk(const T0gGemmSkArgs& kargs) {
             const uint32_t first = tb < it0 ? t0g_sk_worker(total, s.grid, tb) : st.w;
             if (first < st.w) {
                 if (tid == 0) {
+                    const bool stall = (s.debug & T0G_SK_DEBUG_STALL) != 0u;
                     for (uint32_t j = first; j < st.w; ++j) {
+                        gu32_t* const flag = stall ? ctl + T0G_SK_NEVER_SET : ready + j;
                         for (uint32_t n = 0;
-                             __hip_atomic_load(ready + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++n) {
+                             __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++n) {
                             if (n >= s.spin_limit) {
                                 __hip_atomic_fetch_add(ctl + T0G_SK_TIMEOUTS, 1u, __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);

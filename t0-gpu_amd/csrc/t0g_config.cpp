@@ -136,7 +136,7 @@ double model_time_sk_us(uint32_t m, uint32_t k, uint32_t n) {
     return t.t0_us + (double)per_cu * 2.0 * t.bm * t.bn * kTileK / t.rate1 * 1e-3 + (cut ? 30.0 : 5.0);
 }
 
-void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
+void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, bool allow_stream_k) {
     const TileDef *best = &kTiles[0];
     uint32_t best_sk = 1;
     double best_t = 1e300;
@@ -160,7 +160,7 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
     const TileDef &big = kTiles[0];
     const uint64_t tiles256 = (uint64_t)((m + big.bm - 1) / big.bm) * ((n + big.bn - 1) / big.bn);
     const uint64_t last_round = tiles256 % kNumCUs;
-    if (tiles256 > kNumCUs && last_round != 0 && last_round * 8 <= kNumCUs &&
+    if (allow_stream_k && tiles256 > kNumCUs && last_round != 0 && last_round * 8 <= kNumCUs &&
         model_time_sk_us(m, k, n) < 0.85 * best_t) {
         best = &kTiles[0];
         best_sk = T0G_STREAM_K;
@@ -251,6 +251,26 @@ int t0g_config_name(const t0g_gemm_config *cfg, char *buf, size_t len) {
     return ok();
 }
 
+int t0g_tile_config_name(const t0g_gemm_config *cfg, uint32_t chain, char *buf, size_t len) {
+    if (!cfg || !buf || len == 0) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    char epi[64];
+    int rc = t0g_epilogue_chain_name(chain ? chain : legacy_chain(cfg->epilogue), epi, sizeof epi);
+    if (rc) return rc;
+    std::string s = "tile_gemm_" + std::to_string(cfg->tile_m) + "x" + std::to_string(cfg->tile_n) + "_k" +
+                    std::to_string(cfg->tile_k);
+    if (cfg->double_buffer) s += "_db";
+    if (cfg->split_k == T0G_STREAM_K) s += "_streamk";
+    else if (cfg->split_k > 1) s += "_sk" + std::to_string(cfg->split_k);
+    if (!cfg->swap_grid) s += "_mg";
+    if (cfg->wgp_mode) s += "_wgp";
+    static const char *tr[] = {"", "_nn", "_tn", "_tt"};
+    if (cfg->transpose <= T0G_TT) s += tr[cfg->transpose];
+    s += epi;
+    if (s.size() + 1 > len) return fail(T0G_ERR_INVALID_ARG, "name buffer too small (%zu < %zu)", len, s.size() + 1);
+    memcpy(buf, s.c_str(), s.size() + 1);
+    return ok();
+}
+
 int t0g_auto_select(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
     if (!out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
     if (m == 0 || n == 0) return fail(T0G_ERR_INVALID_ARG, "auto_select: m=%u n=%u must be > 0", m, n);
@@ -258,11 +278,19 @@ int t0g_auto_select(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out) {
     return ok();
 }
 
+// The tile ABI runs what t0g_tile_kernel_get + t0g_dispatch launch: NT or NN
+// (TileTranspose has no other layouts, src/t0/tile_ir.rs:73-78), data-parallel
+// or split-K (the library keeps the planes when build_kernargs_m leaves
+// y_split_stride 0), never stream-K.  The reference's table is tuned for 96
+// RDNA3 CUs; the choice here is the same 256-CU model as t0g_auto_select.
 int t0g_tile_auto_select(uint32_t m, uint32_t k, uint32_t n, uint32_t transpose, t0g_gemm_config *out) {
-    if (transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", transpose);
-    int rc = t0g_auto_select(m, k, n, out);
-    if (rc == T0G_OK) out->transpose = transpose;
-    return rc;
+    if (!out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (transpose != T0G_NT && transpose != T0G_NN)
+        return fail(T0G_ERR_INVALID_ARG, "tile ABI layouts are NT and NN (got %u)", transpose);
+    if (m == 0 || n == 0) return fail(T0G_ERR_INVALID_ARG, "tile_auto_select: m=%u n=%u must be > 0", m, n);
+    select_config(m, k, n, out, false);
+    out->transpose = transpose;
+    return ok();
 }
 
 // The stream-K schedule has its own launch shape and argument block: it runs

@@ -39,7 +39,8 @@ const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint
 void make_config(const TileDef &t, uint32_t split_k, t0g_gemm_config *out);
 uint32_t cfg_split(const t0g_gemm_config *cfg);
 int validate(const t0g_gemm_config *cfg);
-void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out);
+// allow_stream_k = false: data-parallel configs only (the tile ABI launches).
+void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, bool allow_stream_k = true);
 double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);
 double model_time_sk_us(uint32_t m, uint32_t k, uint32_t n);   // stream-K, 256x256 tile
 
@@ -53,6 +54,19 @@ uint32_t chain_kernarg_bytes(uint32_t chain);      // tile_ir arguments after M
 // Device time (ms) of each of `iters` t0g_gemm launches of d, after `warmup`
 // untimed ones (t0g_runtime.cpp).
 int time_gemm(t0g_device *dev, const t0g_gemm_desc *d, uint32_t warmup, uint32_t iters, std::vector<double> *ms);
+
+// One kernel's entry in a code object's AMDGPU metadata (t0g_codeobj.cpp).
+struct KernelMeta {
+    uint32_t explicit_args_size;     // end of the last non-hidden argument: the caller's block
+    uint32_t kernarg_segment_size;   // with the hidden arguments the runtime appends
+    uint32_t group_segment_size;     // static LDS bytes
+    uint32_t private_segment_size;   // scratch bytes per lane
+    uint32_t max_workgroup_size;
+    uint32_t wavefront_size;
+};
+// Metadata of kernel `symbol` in a gfx950 code object (bare ELF or clang
+// offload bundle); refuses objects for other GPUs and malformed input.
+int read_kernel_meta(const void *code_object, size_t size, const char *symbol, KernelMeta *out);
 
 }  // namespace t0g
 

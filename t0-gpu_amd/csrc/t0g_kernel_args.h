@@ -41,7 +41,8 @@ typedef struct T0gGemmSkArgs {
     uint32_t grid;           /* launched workgroups, <= tiles * iters_per_tile    */
     uint32_t iters_per_tile; /* ceil(k / 64)                                      */
     uint32_t spin_limit;     /* polls of a ready flag before counting a timeout   */
-    uint32_t reserved[3];    /* pads the block to 144 bytes (whole 16-byte words) */
+    uint32_t debug;          /* T0G_SK_DEBUG_* bits (0 in normal use)             */
+    uint32_t reserved[2];    /* pads the block to 144 bytes (whole 16-byte words) */
 } T0gGemmSkArgs;
 
 #define T0G_SK_TILE 256u
@@ -51,6 +52,10 @@ typedef struct T0gGemmSkArgs {
 #define T0G_SK_DONE 1u           /* control word: finished workgroups                 */
 #define T0G_SK_TIMEOUTS 2u       /* control word: ready-flag waits that gave up, and
                                     workgroups that drew a ticket past the grid       */
+#define T0G_SK_NEVER_SET 3u      /* control word nothing writes (stays 0)             */
+#define T0G_SK_DEBUG_STALL 1u    /* owners wait on T0G_SK_NEVER_SET instead of the ready
+                                    flags, so every wait runs to its spin limit and gives
+                                    up: a host-forced timeout for testing error reporting */
 
 #if defined(__HIPCC__)
 #define T0G_HD __host__ __device__

@@ -51,7 +51,8 @@ struct t0g_kernel {
     hipFunction_t fn = nullptr;   // Raw
     uint32_t wg[3] = {1, 1, 1};
     uint32_t lds = 0;
-    uint32_t kernarg_size = 0;
+    uint32_t dyn_lds = 0;         // Raw: LDS requested at launch beyond the kernel's static LDS
+    uint32_t kernarg_size = 0;    // Raw: exact argument block size, from the code object's metadata
     uint32_t chain = 0;           // TileGemm: epilogue chain its kernargs carry
     std::string name;
 };
@@ -68,13 +69,18 @@ struct t0g_device {
     std::vector<std::unique_ptr<t0g_kernel>> kernels;
     std::unordered_map<std::string, t0g_kernel *> kernel_cache;
     std::vector<hipModule_t> extra_modules;
-    std::set<uint64_t> allocations;
+    std::unordered_map<uint64_t, size_t> allocations;   // live buffers -> their 4 KiB-rounded size
+    // BufferPool (src/ignis/gpu_context.rs:21-76): recycled buffers by size
+    std::unordered_map<size_t, std::vector<uint64_t>> pool;
+    size_t pool_bytes = 0;
+    uint64_t pool_hits = 0, pool_misses = 0;
     uint64_t ws = 0;
     size_t ws_bytes = 0;
     uint64_t conv = 0;         // bf16 operand scratch of the matmul entry points
     size_t conv_bytes = 0;
     uint32_t num_cus = 0;      // compute units: the stream-K grid
     uint64_t sk_sync = 0;      // stream-K control words and ready flags (zero between launches)
+    hipStream_t sk_stream = nullptr;   // stream of a stream-K launch whose timeout word is not yet checked
     // t0g_gemm_group: side streams (default priority), each with its own split-K
     // workspace, and the events that fork them from and join them back into `stream`
     static constexpr int kSides = 2;
@@ -89,6 +95,11 @@ namespace t0g {
 
 static std::atomic<int> g_fail_countdown{0};
 static std::atomic<uint32_t> g_wait_timeout_ms{60000};
+// Polls of a stream-K ready flag (each followed by a short s_sleep: about a
+// tenth of a second in all at the default, against microseconds for a real
+// wait) before a workgroup gives up and counts a timeout.
+static std::atomic<uint32_t> g_sk_spin_limit{1u << 20};
+static std::atomic<uint32_t> g_sk_debug{0};
 
 // Every HIP call goes through here so a test can make the n-th one fail.
 static bool injected_failure() {
@@ -129,6 +140,26 @@ static double now_ms() {
     return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
 }
 
+// Once a stream that ran a stream-K launch has drained: a ready-flag wait that
+// gave up, or a launch that found the control block busy, left cut tiles
+// without some of their partial sums, so the result is wrong and the device is
+// poisoned with T0G_ERR_TIMEOUT, as the reference poisons its runtime after a
+// dispatch timeout (src/ignis/gpu_context.rs:150-157).
+static int check_stream_k(t0g_device *dev) {
+    if (!dev->sk_stream || dev->sk_stream != dev->stream) return T0G_OK;
+    dev->sk_stream = nullptr;
+    uint32_t count = 0;
+    hipError_t e = T0G_HIP(hipMemcpy(&count, (const void *)(dev->sk_sync + 4 * T0G_SK_TIMEOUTS), 4,
+                                     hipMemcpyDeviceToHost));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemcpy(stream-K timeout count)"));
+    if (count)
+        return poison(dev, fail(T0G_ERR_TIMEOUT,
+                                "stream-K: %u ready-flag wait(s) gave up or launches overlapped; cut tiles miss "
+                                "partial sums",
+                                count));
+    return T0G_OK;
+}
+
 // Wait for the stream with a time limit (the reference polls the AQL read
 // pointer for 5 s, src/kfd/mod.rs:1607-1642).  Timeout poisons the device.
 static int wait_stream(t0g_device *dev) {
@@ -136,7 +167,7 @@ static int wait_stream(t0g_device *dev) {
     const uint32_t limit = g_wait_timeout_ms.load();
     for (;;) {
         hipError_t e = T0G_HIP(hipStreamQuery(dev->stream));
-        if (e == hipSuccess) return T0G_OK;
+        if (e == hipSuccess) return check_stream_k(dev);
         if (e != hipErrorNotReady) return poison(dev, hip_fail(e, "hipStreamQuery"));
         if (now_ms() - t0 > limit)
             return poison(dev, fail(T0G_ERR_TIMEOUT, "GPU wait timed out after %u ms", limit));
@@ -312,11 +343,6 @@ struct GemmOperands {
     uint64_t c_split_stride;   // reference-layout path: caller-owned planes
 };
 
-// Polls of a stream-K ready flag (each followed by a short s_sleep: about a
-// tenth of a second in all, against microseconds for a real wait) before a
-// workgroup gives up and counts a timeout.
-constexpr uint32_t kSkSpinLimit = 1u << 20;
-
 // Stream-K control words and ready flags, allocated and zeroed once per device;
 // every launch leaves them zero again.
 static int ensure_sk_sync(t0g_device *dev) {
@@ -334,13 +360,11 @@ static int ensure_sk_sync(t0g_device *dev) {
     return T0G_OK;
 }
 
-// Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
-// the partial planes go to `ws` and the reduce kernel produces C.
-static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws) {
-    hipFunction_t f = nullptr;
-    int rc = get_function(dev, p.symbol, &f);
-    if (rc) return rc;
-    T0gGemmArgs args;
+// The GEMM kernel's argument block for a plan.  With splits > 1 and no
+// caller-owned planes (o.c_split_stride == 0) the kernel writes fp32 planes to
+// `ws` and *reduce is set: the reduce kernel then produces C.
+static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws, T0gGemmArgs *out, bool *reduce_out) {
+    T0gGemmArgs &args = *out;
     memset(&args, 0, sizeof args);
     args.a = o.a;
     args.b = o.b;
@@ -374,6 +398,18 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     const uint64_t esize = reduce || !p.out_bf16 ? 4 : 2;
     if ((args.c & 15) == 0 && ((uint64_t)args.ldc * esize) % 16 == 0 && args.c_split_stride % 16 == 0)
         args.flags |= T0G_FLAG_C_VEC;
+    *reduce_out = reduce;
+}
+
+// Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
+// the partial planes go to `ws` and the reduce kernel produces C.
+static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws) {
+    hipFunction_t f = nullptr;
+    int rc = get_function(dev, p.symbol, &f);
+    if (rc) return rc;
+    T0gGemmArgs args;
+    bool reduce = false;
+    fill_gemm_args(p, o, ws, &args, &reduce);
     if (p.stream_k) {
         T0gGemmSkArgs sa;
         memset(&sa, 0, sizeof sa);
@@ -382,7 +418,9 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
         sa.sync = dev->sk_sync;
         sa.grid = sk_grid(p, dev->num_cus);
         sa.iters_per_tile = p.sk_ipt;
-        sa.spin_limit = kSkSpinLimit;
+        sa.spin_limit = g_sk_spin_limit.load();
+        sa.debug = g_sk_debug.load();
+        dev->sk_stream = dev->stream;
         return launch(dev, f, sa.grid, 1, 1, p.wg, &sa, sizeof sa);
     }
     rc = launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.wg, &args, sizeof args);
@@ -509,6 +547,16 @@ int t0g_set_wait_timeout_ms(uint32_t ms) {
     return ok();
 }
 
+int t0g_set_stream_k_spin_limit(uint32_t polls) {
+    g_sk_spin_limit.store(polls);
+    return ok();
+}
+
+int t0g_debug_stream_k_stall(int on) {
+    g_sk_debug.store(on ? T0G_SK_DEBUG_STALL : 0u);
+    return ok();
+}
+
 int t0g_device_count(int *count) {
     if (!count) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
     int n = 0;
@@ -567,7 +615,9 @@ int t0g_device_close(t0g_device *dev) {
         if (dev->join_ev[i]) (void)hipEventDestroy(dev->join_ev[i]);
     }
     if (dev->fork_ev) (void)hipEventDestroy(dev->fork_ev);
-    for (uint64_t a : dev->allocations) (void)hipFree((void *)a);
+    for (const auto &a : dev->allocations) (void)hipFree((void *)a.first);
+    for (const auto &bucket : dev->pool)
+        for (uint64_t a : bucket.second) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
     if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
@@ -594,17 +644,35 @@ int t0g_device_is_poisoned(t0g_device *dev, int *poisoned) {
     return ok();
 }
 
+// The pool's size key: whole 4 KiB pages, as BufferPool::alloc rounds.
+static size_t pool_size(size_t bytes) { return ((bytes ? bytes : 1) + 4095) & ~(size_t)4095; }
+
+static int alloc_locked(t0g_device *dev, size_t bytes, uint64_t *addr) {
+    const size_t size = pool_size(bytes);
+    auto it = dev->pool.find(size);
+    if (it != dev->pool.end() && !it->second.empty()) {
+        *addr = it->second.back();
+        it->second.pop_back();
+        dev->pool_bytes -= size;
+        dev->pool_hits++;
+    } else {
+        void *p = nullptr;
+        hipError_t e = T0G_HIP(hipMalloc(&p, size));
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+        *addr = (uint64_t)p;
+        dev->pool_misses++;
+    }
+    dev->allocations[*addr] = size;
+    return T0G_OK;
+}
+
 int t0g_alloc(t0g_device *dev, size_t bytes, uint64_t *addr) {
     if (!dev || !addr) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
     *addr = 0;
     std::lock_guard<std::mutex> lk(dev->mu);
     int rc = check_usable(dev);
     if (rc) return rc;
-    void *p = nullptr;
-    hipError_t e = T0G_HIP(hipMalloc(&p, bytes ? bytes : 1));
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
-    dev->allocations.insert((uint64_t)p);
-    *addr = (uint64_t)p;
+    if ((rc = alloc_locked(dev, bytes, addr))) return rc;
     return ok();
 }
 
@@ -617,7 +685,9 @@ int t0g_alloc_zero(t0g_device *dev, size_t bytes, uint64_t *addr) {
 int t0g_free(t0g_device *dev, uint64_t addr) {
     if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
     std::lock_guard<std::mutex> lk(dev->mu);
-    if (!dev->allocations.count(addr)) return fail(T0G_ERR_INVALID_ARG, "0x%llx was not allocated by t0g_alloc", (unsigned long long)addr);
+    if (!dev->allocations.count(addr))
+        return fail(T0G_ERR_INVALID_ARG, "0x%llx is not a live buffer of t0g_alloc (never allocated, freed or recycled)",
+                    (unsigned long long)addr);
     (void)hipSetDevice(dev->ordinal);
     if (!dev->poisoned) {
         int rc = wait_stream(dev);   // the reference frees without waiting (src/kfd/mod.rs:1057-1081)
@@ -626,6 +696,93 @@ int t0g_free(t0g_device *dev, uint64_t addr) {
     dev->allocations.erase(addr);
     hipError_t e = T0G_HIP(hipFree((void *)addr));
     if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return ok();
+}
+
+int t0g_recycle(t0g_device *dev, uint64_t addr) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    auto it = dev->allocations.find(addr);
+    if (it == dev->allocations.end())
+        return fail(T0G_ERR_INVALID_ARG, "0x%llx is not a live buffer of t0g_alloc (never allocated, freed or recycled)",
+                    (unsigned long long)addr);
+    const size_t size = it->second;
+    dev->allocations.erase(it);
+    dev->pool[size].push_back(addr);
+    dev->pool_bytes += size;
+    return ok();
+}
+
+int t0g_pool_clear(t0g_device *dev) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    (void)hipSetDevice(dev->ordinal);
+    if (!dev->poisoned) {
+        int rc = wait_stream(dev);   // recycled buffers may still be read by queued work
+        if (rc) return rc;
+    }
+    hipError_t first = hipSuccess;
+    for (auto &bucket : dev->pool)
+        for (uint64_t a : bucket.second) {
+            hipError_t e = T0G_HIP(hipFree((void *)a));
+            if (e != hipSuccess && first == hipSuccess) first = e;
+        }
+    dev->pool.clear();
+    dev->pool_bytes = 0;
+    if (first != hipSuccess) return hip_fail(first, "hipFree(pooled buffer)");
+    return ok();
+}
+
+int t0g_pool_stats(t0g_device *dev, t0g_pool_info *out) {
+    if (!dev || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    memset(out, 0, sizeof *out);
+    out->cached_bytes = dev->pool_bytes;
+    for (const auto &bucket : dev->pool) out->cached_buffers += bucket.second.size();
+    out->live_buffers = dev->allocations.size();
+    for (const auto &a : dev->allocations) out->live_bytes += a.second;
+    out->hits = dev->pool_hits;
+    out->misses = dev->pool_misses;
+    return ok();
+}
+
+// alloc_f32 pads to whole 512-byte blocks, at least one (src/ignis/gpu_context.rs:449-454).
+static size_t f32_bytes(size_t n) { return ((n * 4 > 512 ? n * 4 : 512) + 511) & ~(size_t)511; }
+
+int t0g_alloc_f32(t0g_device *dev, size_t n, uint64_t *addr) {
+    if (!dev || !addr) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *addr = 0;
+    if (n > (SIZE_MAX - 1024) / 4) return fail(T0G_ERR_INVALID_ARG, "%zu floats overflow a size", n);
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    const size_t bytes = f32_bytes(n);
+    if ((rc = alloc_locked(dev, bytes, addr))) return rc;
+    // zeroed in stream order: work enqueued later on the device stream sees zeros
+    hipError_t e = T0G_HIP(hipMemsetAsync((void *)*addr, 0, bytes, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemsetAsync"));
+    return ok();
+}
+
+int t0g_write_f32(t0g_device *dev, uint64_t addr, const float *src, size_t n) {
+    if (n > SIZE_MAX / 4) return fail(T0G_ERR_INVALID_ARG, "%zu floats overflow a size", n);
+    return t0g_memcpy_h2d(dev, addr, src, n * 4);
+}
+
+int t0g_read_f32(t0g_device *dev, uint64_t addr, float *dst, size_t n) {
+    if (n > SIZE_MAX / 4) return fail(T0G_ERR_INVALID_ARG, "%zu floats overflow a size", n);
+    return t0g_memcpy_d2h(dev, dst, addr, n * 4);   // waits for the stream first, as read_f32 waits for idle
+}
+
+int t0g_upload_f32(t0g_device *dev, const float *src, size_t n, uint64_t *addr) {
+    if (!addr || (!src && n)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    int rc = t0g_alloc_f32(dev, n, addr);
+    if (rc) return rc;
+    if ((rc = t0g_write_f32(dev, *addr, src, n))) {
+        (void)t0g_recycle(dev, *addr);
+        *addr = 0;
+        return rc;
+    }
     return ok();
 }
 
@@ -720,11 +877,19 @@ int t0g_tile_kernel_get_epilogue(t0g_device *dev, const t0g_gemm_config *cfg, ui
 int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size, const char *symbol,
                     const uint32_t workgroup_size[3], uint32_t lds_size, t0g_kernel **out) {
     if (!dev || !code_object || !symbol || !workgroup_size || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
-    (void)size;
     *out = nullptr;
-    std::lock_guard<std::mutex> lk(dev->mu);
-    int rc = check_usable(dev);
+    // The argument size, LDS and largest workgroup come from the code object,
+    // so a dispatch that does not fit the kernel is refused on the host.
+    KernelMeta meta;
+    int rc = read_kernel_meta(code_object, size, symbol, &meta);
     if (rc) return rc;
+    uint64_t threads = 1;
+    for (int i = 0; i < 3; i++) threads *= workgroup_size[i] ? workgroup_size[i] : 1;
+    if (threads > meta.max_workgroup_size)
+        return fail(T0G_ERR_INVALID_ARG, "workgroup of %llu threads; %s was built for at most %u",
+                    (unsigned long long)threads, symbol, meta.max_workgroup_size);
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if ((rc = check_usable(dev))) return rc;
     hipModule_t m = nullptr;
     hipError_t e = T0G_HIP(hipModuleLoadData(&m, code_object));
     if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
@@ -740,8 +905,9 @@ int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size, const
     memset(&k->cfg, 0, sizeof k->cfg);
     k->fn = f;
     for (int i = 0; i < 3; i++) k->wg[i] = workgroup_size[i] ? workgroup_size[i] : 1;
-    k->lds = lds_size;
-    k->kernarg_size = 0;
+    k->lds = lds_size > meta.group_segment_size ? lds_size : meta.group_segment_size;
+    k->dyn_lds = lds_size > meta.group_segment_size ? lds_size - meta.group_segment_size : 0;
+    k->kernarg_size = meta.explicit_args_size;
     k->name = symbol;
     *out = k.get();
     dev->kernels.push_back(std::move(k));
@@ -820,7 +986,12 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
     o.lda = o.k;
     o.ldb = cfg.transpose == T0G_NN ? o.n : o.k;
     o.ldc = o.n;
-    if (sk > 1) {
+    // tile_ir split-K: build_kernargs_m always writes y_split_stride = 0 and
+    // leaves the planes to the caller (src/t0/tile_ir.rs:3154-3157, 3179), so a
+    // stride of 0 here means the library keeps the fp32 planes in its own
+    // workspace and reduces them into Y in plane order, epilogue chain last.
+    const bool lib_planes = kn->kind == KernelKind::TileGemm && sk > 1 && y_split_stride == 0;
+    if (sk > 1 && !lib_planes) {
         if (y_split_stride == 0)
             return fail(T0G_ERR_INVALID_ARG,
                         "split_k=%u with y_split_stride=0 would make every K slice store to the same Y", sk);
@@ -828,6 +999,12 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
             return fail(T0G_ERR_UNSUPPORTED_CONFIG, "K=%u must be a multiple of tile_k*split_k=%u", o.k, sk * kTileK);
         if ((uint64_t)y_split_stride < (uint64_t)o.m * o.n * 4)
             return fail(T0G_ERR_INVALID_ARG, "y_split_stride=%u smaller than one M*N f32 plane", y_split_stride);
+        // the reference's kernel would apply the epilogue to every partial plane
+        // (bias added split_k times); the planes stay plain partial sums here
+        if (o.chain != 0)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG,
+                        "an epilogue on caller-owned split-K planes would be applied to every partial sum; "
+                        "leave y_split_stride 0 (tile ABI) for a reduced, epilogued Y");
         o.c_split_stride = y_split_stride;
     }
     int rc;
@@ -844,6 +1021,20 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
                     "tile %ux%u cannot take these operands (rows must be 16-byte aligned with K %% 8 == 0; "
                     "operands of 2^30 elements or more need the 256x256 tile)",
                     cfg.tile_m, cfg.tile_n);
+    if (lib_planes) {
+        // the plan's own split of K (any K); the grid must cover the whole output,
+        // since the reduce reads every element of the planes
+        if (tiles_m < p.tiles_m || tiles_n < p.tiles_n)
+            return fail(T0G_ERR_INVALID_ARG, "grid covers %ux%u tiles; split-K over %ux%u needs %ux%u", tiles_m,
+                        tiles_n, o.m, o.n, p.tiles_m, p.tiles_n);
+        if (o.m == 0 || o.n == 0) return ok();
+        uint64_t ws = 0;
+        if (p.splits > 1) {
+            if ((rc = ensure_workspace(dev, (size_t)p.splits * o.m * o.n * 4))) return rc;
+            ws = dev->ws;
+        }
+        return run_plan(dev, p, o, ws);
+    }
     p.tiles_m = tiles_m;
     p.tiles_n = tiles_n;
     p.splits = sk;
@@ -863,12 +1054,15 @@ static int dispatch_common(t0g_device *dev, const t0g_kernel *kernel, const uint
         if (grid[0] % bx || grid[1] % by || grid[2] % bz)
             return fail(T0G_ERR_INVALID_ARG, "grid (%u,%u,%u) is not a multiple of the workgroup", grid[0], grid[1],
                         grid[2]);
+        if (len != kernel->kernarg_size)
+            return fail(T0G_ERR_INVALID_ARG, "kernargs are %zu bytes; %s takes exactly %u (code object metadata)", len,
+                        kernel->name.c_str(), kernel->kernarg_size);
         std::vector<uint8_t> buf((const uint8_t *)ka, (const uint8_t *)ka + len);
         size_t sz = len;
         void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, buf.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
                          HIP_LAUNCH_PARAM_END};
         hipError_t e = T0G_HIP(hipModuleLaunchKernel(kernel->fn, grid[0] / bx, grid[1] / by, grid[2] / bz, bx, by, bz,
-                                                     kernel->lds, dev->stream, nullptr, extra));
+                                                     kernel->dyn_lds, dev->stream, nullptr, extra));
         if (e != hipSuccess) return poison(dev, hip_fail(e, "hipModuleLaunchKernel"));
     } else {
         rc = dispatch_gemm(dev, kernel, grid, (const uint8_t *)ka, len);
@@ -919,6 +1113,60 @@ int t0g_gemm_kernel_name(const t0g_gemm_desc *d, char *buf, size_t len) {
     int rc = resolve_desc(d, &cfg, &p, &o);
     if (rc) return rc;
     snprintf(buf, len, "%s", p.symbol.c_str());
+    return ok();
+}
+
+int t0g_gemm_compile(const t0g_gemm_desc *d, t0g_compiled_kernel *out) {
+    if (!d || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    memset(out, 0, sizeof *out);
+    t0g_gemm_config cfg;
+    GemmPlan p;
+    GemmOperands o;
+    int rc = resolve_desc(d, &cfg, &p, &o);
+    if (rc) return rc;
+    // Planes go into C, so C's size must not depend on a split the caller did not
+    // ask for: a split comes only from desc->split_k or an explicit config.  An
+    // auto-selected split, or stream-K (its launches need the device's flag
+    // words), compiles as the same tile without the split.
+    const bool asked = d->split_k > 1 || (d->split_k == 0 && d->config && cfg_split(d->config) > 1 &&
+                                          d->config->split_k != T0G_STREAM_K);
+    if (p.stream_k || (p.splits > 1 && !asked)) {
+        t0g_gemm_config dp = cfg;
+        dp.split_k = 0;
+        t0g_gemm_desc d2 = *d;
+        d2.config = &dp;
+        d2.split_k = 1;
+        if ((rc = resolve_desc(&d2, &cfg, &p, &o))) return rc;
+    }
+    if (p.splits > 1) {
+        if (d->out_dtype != T0G_F32)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "a split-K kernel writes fp32 planes: out_dtype must be F32");
+        if (o.chain)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "an epilogue cannot be applied to split-K partial planes");
+        o.c_split_stride = (uint64_t)o.m * o.ldc * 4;
+    }
+    if ((uint64_t)p.tiles_m * p.tiles_n * p.wg > 0xFFFFFFFFull)
+        return fail(T0G_ERR_INVALID_ARG, "%u x %u tiles: the grid in threads exceeds 32 bits", p.tiles_m, p.tiles_n);
+    T0gGemmArgs args;
+    bool reduce = false;
+    fill_gemm_args(p, o, 0, &args, &reduce);
+    const size_t co_size = (size_t)(t0g_hsaco_end - t0g_hsaco_begin);
+    KernelMeta meta;
+    if ((rc = read_kernel_meta(t0g_hsaco_begin, co_size, p.symbol.c_str(), &meta))) return rc;
+    if (meta.explicit_args_size != sizeof args)
+        return fail(T0G_ERR_HIP, "%s takes %u argument bytes, this library builds %zu", p.symbol.c_str(),
+                    meta.explicit_args_size, sizeof args);
+    out->code_object = t0g_hsaco_begin;
+    out->code_object_size = co_size;
+    snprintf(out->name, sizeof out->name, "%s", p.symbol.c_str());
+    out->workgroup_size = p.wg;
+    out->lds_size = meta.group_segment_size;
+    out->kernarg_size = (uint32_t)sizeof args;
+    out->grid[0] = p.tiles_m * p.tiles_n * p.wg;
+    out->grid[1] = p.splits;
+    out->grid[2] = 1;
+    out->splits = p.splits;
+    memcpy(out->kernargs, &args, sizeof args);
     return ok();
 }
 
@@ -995,9 +1243,14 @@ int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n) {
     for (int i = 0; i < sides; ++i)
         if ((e = T0G_HIP(hipStreamWaitEvent(dev->side[i], dev->fork_ev, 0))) != hipSuccess)
             return poison(dev, hip_fail(e, "hipStreamWaitEvent(fork)"));
-    const hipStream_t main_stream = dev->stream;
-    const uint64_t main_ws = dev->ws;
-    const size_t main_ws_bytes = dev->ws_bytes;
+    // A side stream's GEMM runs with that stream's workspace swapped into
+    // dev->ws, and the slots are swapped back afterwards, so a workspace that a
+    // GEMM grows (freeing the old one) is kept by whichever stream grew it.
+    auto swap_side = [dev](int s) {
+        std::swap(dev->stream, dev->side[s]);
+        std::swap(dev->ws, dev->side_ws[s]);
+        std::swap(dev->ws_bytes, dev->side_ws_bytes[s]);
+    };
     int first_rc = T0G_OK;
     for (uint32_t i = 0; i < n && !first_rc; ++i) {
         t0g_gemm_desc d = descs[i];
@@ -1013,19 +1266,9 @@ int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n) {
             d.split_k = 1;
         }
         const int s = (int)(i % (uint32_t)(sides + 1)) - 1;   // -1: the device stream
-        if (s >= 0) {
-            dev->stream = dev->side[s];
-            dev->ws = dev->side_ws[s];
-            dev->ws_bytes = dev->side_ws_bytes[s];
-        }
+        if (s >= 0) swap_side(s);
         first_rc = gemm_locked(dev, &d);
-        if (s >= 0) {
-            dev->side_ws[s] = dev->ws;
-            dev->side_ws_bytes[s] = dev->ws_bytes;
-            dev->stream = main_stream;
-            dev->ws = main_ws;
-            dev->ws_bytes = main_ws_bytes;
-        }
+        if (s >= 0) swap_side(s);
     }
     // join whatever was enqueued, also after a failure
     for (int i = 0; i < sides; ++i) {

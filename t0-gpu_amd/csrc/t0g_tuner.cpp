@@ -9,6 +9,10 @@
 // synchronous dispatch), operands hold random bf16 data (all-zero operands
 // let a power-limited GPU clock higher than real data does, which skews the
 // ranking), and all candidates share one set of buffers.
+//
+// The same tuner also serves tune_tile_ir (src/t0/cost_model.rs:757-1013):
+// the tile ABI's configs (NT, f32 out, no stream-K), cached as
+// tile_ir_MxNxK.json with that file's keys (cost_model.rs:1030-1097).
 #include <errno.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -31,10 +35,15 @@
 namespace t0g {
 namespace {
 
+// Which tuner a result belongs to: GemmTuner (gemm_*.json) or tune_tile_ir
+// (tile_ir_*.json, NT with f32 output only).
+enum TuneKind : uint32_t { kGemm = 0, kTileIr = 1 };
+
 struct TuneKey {
     uint32_t m, n, k, transpose, out_dtype;
+    uint32_t kind = kGemm;
     bool operator<(const TuneKey &o) const {
-        return std::tie(m, n, k, transpose, out_dtype) < std::tie(o.m, o.n, o.k, o.transpose, o.out_dtype);
+        return std::tie(kind, m, n, k, transpose, out_dtype) < std::tie(o.kind, o.m, o.n, o.k, o.transpose, o.out_dtype);
     }
 };
 
@@ -62,6 +71,16 @@ std::string config_name(const t0g_gemm_config &cfg) {
     char buf[128];
     if (t0g_config_name(&cfg, buf, sizeof buf)) return "?";
     return buf;
+}
+
+std::string tile_name(const t0g_gemm_config &cfg) {
+    char buf[128];
+    if (t0g_tile_config_name(&cfg, 0, buf, sizeof buf)) return "?";
+    return buf;
+}
+
+std::string entry_name(const TuneKey &key, const t0g_gemm_config &cfg) {
+    return key.kind == kTileIr ? tile_name(cfg) : config_name(cfg);
 }
 
 // mkdir -p
@@ -223,6 +242,9 @@ namespace t0g {
 namespace {
 
 std::string cache_path(const t0g_tuner *t, const TuneKey &key) {
+    if (key.kind == kTileIr)   // tile_ir_cache_path (cost_model.rs:1068-1070)
+        return t->dir + "/tile_ir_" + std::to_string(key.m) + "x" + std::to_string(key.n) + "x" +
+               std::to_string(key.k) + ".json";
     std::string p = t->dir + "/gemm_" + std::to_string(key.m) + "x" + std::to_string(key.n) + "x" +
                     std::to_string(key.k);
     if (key.transpose != T0G_NT) p += std::string("_") + kLayoutTag[key.transpose];
@@ -252,9 +274,14 @@ bool load_entry(const t0g_tuner *t, const TuneKey &key, TuneEntry *e) {
     memset(&cfg, 0, sizeof cfg);
     double tflops = 0;
     if (!read_u32(js, "tile_m", &cfg.tile_m) || !read_u32(js, "tile_n", &cfg.tile_n) ||
-        !read_u32(js, "tile_k", &cfg.tile_k) || !read_u32(js, "wg_size", &cfg.wg_size) ||
-        !read_f64(js, "tflops", &tflops))
+        !read_u32(js, "tile_k", &cfg.tile_k) || !read_f64(js, "tflops", &tflops))
         return false;
+    if (!read_u32(js, "wg_size", &cfg.wg_size)) {
+        // load_tile_ir_cache's keys have no workgroup size: the tile implies it
+        if (key.kind != kTileIr) return false;
+        for (const TileDef &td : kTiles)
+            if (td.bm == cfg.tile_m && td.bn == cfg.tile_n) cfg.wg_size = td.wg;
+    }
     uint32_t sk = 1;
     read_u32(js, "split_k", &sk);
     cfg.split_k = sk > 1 ? sk : 0;
@@ -269,6 +296,7 @@ bool load_entry(const t0g_tuner *t, const TuneKey &key, TuneEntry *e) {
     cfg.transpose = key.transpose;
     cfg.epilogue = T0G_EPI_STORE_F32;
     if (validate(&cfg)) return false;
+    if (key.kind == kTileIr && cfg.split_k == T0G_STREAM_K) return false;
     if (!read_ranking(js, &e->all)) e->all.clear();
     memset(&e->result, 0, sizeof e->result);
     e->result.best = cfg;
@@ -291,13 +319,21 @@ int save_entry(const t0g_tuner *t, const TuneKey &key, const TuneEntry &e) {
     const t0g_gemm_config &c = e.result.best;
     std::string js;
     char buf[512];
-    snprintf(buf, sizeof buf,
-             "{\"tile_m\":%u,\"tile_n\":%u,\"tile_k\":%u,\"wg_size\":%u,\"split_k\":%u,\"lds_pad\":%u,"
-             "\"n_col_passes\":%u,\"wgp\":%s,\"swap\":%s,\"tflops\":%.2f,\"arch\":\"gfx950\",\"layout\":\"%s\","
-             "\"out\":\"%s\",\"m\":%u,\"n\":%u,\"k\":%u,\"all\":[",
-             c.tile_m, c.tile_n, c.tile_k, c.wg_size, c.split_k > 1 ? c.split_k : 1, c.lds_pad, c.n_col_passes,
-             c.wgp_mode ? "true" : "false", c.swap_grid ? "true" : "false", e.result.best_tflops,
-             kLayoutTag[key.transpose], key.out_dtype == T0G_BF16 ? "bf16" : "f32", key.m, key.n, key.k);
+    if (key.kind == kTileIr)   // save_tile_ir_cache's keys (cost_model.rs:1076-1093), then ours
+        snprintf(buf, sizeof buf,
+                 "{\"tile_m\":%u,\"tile_n\":%u,\"tile_k\":%u,\"split_k\":%u,\"wgp\":%s,\"tflops\":%.2f,"
+                 "\"arch\":\"gfx950\",\"wg_size\":%u,\"layout\":\"%s\",\"out\":\"f32\",\"m\":%u,\"n\":%u,"
+                 "\"k\":%u,\"all\":[",
+                 c.tile_m, c.tile_n, c.tile_k, c.split_k > 1 ? c.split_k : 1, c.wgp_mode ? "true" : "false",
+                 e.result.best_tflops, c.wg_size, kLayoutTag[key.transpose], key.m, key.n, key.k);
+    else
+        snprintf(buf, sizeof buf,
+                 "{\"tile_m\":%u,\"tile_n\":%u,\"tile_k\":%u,\"wg_size\":%u,\"split_k\":%u,\"lds_pad\":%u,"
+                 "\"n_col_passes\":%u,\"wgp\":%s,\"swap\":%s,\"tflops\":%.2f,\"arch\":\"gfx950\",\"layout\":\"%s\","
+                 "\"out\":\"%s\",\"m\":%u,\"n\":%u,\"k\":%u,\"all\":[",
+                 c.tile_m, c.tile_n, c.tile_k, c.wg_size, c.split_k > 1 ? c.split_k : 1, c.lds_pad, c.n_col_passes,
+                 c.wgp_mode ? "true" : "false", c.swap_grid ? "true" : "false", e.result.best_tflops,
+                 kLayoutTag[key.transpose], key.out_dtype == T0G_BF16 ? "bf16" : "f32", key.m, key.n, key.k);
     js = buf;
     for (size_t i = 0; i < e.all.size(); ++i) {
         snprintf(buf, sizeof buf, "%s[\"%s\",%.2f]", i ? "," : "", e.all[i].first.c_str(), e.all[i].second);
@@ -329,7 +365,9 @@ const TuneEntry *find_entry(t0g_tuner *t, const TuneKey &key) {
     return &(t->cache[key] = std::move(e));
 }
 
-void candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, std::vector<t0g_gemm_config> *out) {
+// with_stream_k = false for the tile ABI, which has no stream-K launch.
+void candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, std::vector<t0g_gemm_config> *out,
+                bool with_stream_k = true) {
     struct Cand {
         double t;
         int order;
@@ -348,7 +386,7 @@ void candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, std::vec
             all.push_back(c);
         }
     }
-    {
+    if (with_stream_k) {
         // stream-K, ranked with the margin auto_select demands of it
         Cand c;
         c.t = model_time_sk_us(m, k, n) / 0.85;
@@ -368,7 +406,7 @@ int tune_locked(t0g_tuner *t, t0g_device *dev, const TuneKey &key, const TuneEnt
         return T0G_OK;
     }
     std::vector<t0g_gemm_config> cands;
-    candidates(key.m, key.n, key.k, key.transpose, &cands);
+    candidates(key.m, key.n, key.k, key.transpose, &cands, key.kind != kTileIr);
     if (cands.size() > t->max_candidates) cands.resize(t->max_candidates);
 
     const size_t a_elems = (size_t)key.m * key.k, b_elems = (size_t)key.n * key.k;
@@ -419,7 +457,7 @@ int tune_locked(t0g_tuner *t, t0g_device *dev, const TuneKey &key, const TuneEnt
             std::vector<double> ms;
             int brc = time_gemm(dev, &d, warm, t->n_iters, &ms);
             if (brc) {
-                last_failure = config_name(cands[i]) + ": " + g_last_error;
+                last_failure = entry_name(key, cands[i]) + ": " + g_last_error;
                 failed[i] = 1;
                 int poisoned = 0;
                 if (t0g_device_is_poisoned(dev, &poisoned) == T0G_OK && poisoned) {
@@ -460,7 +498,7 @@ int tune_locked(t0g_tuner *t, t0g_device *dev, const TuneKey &key, const TuneEnt
     e.result.transpose = key.transpose;
     e.result.out_dtype = key.out_dtype;
     e.result.from_cache = 0;
-    for (const auto &r : results) e.all.emplace_back(config_name(r.first), r.second);
+    for (const auto &r : results) e.all.emplace_back(entry_name(key, r.first), r.second);
     e.result.n_all = (uint32_t)e.all.size();
     // A cache directory that cannot be written costs the persistence, not the result
     // (the reference only logs the failed write).
@@ -619,8 +657,8 @@ int t0g_tuner_invalidate(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, u
 }
 
 // clear (auto_gemm.rs:400-403) removes the whole directory; here only the
-// files this tuner writes (gemm_*.json) and then the directory if it is empty,
-// so a directory shared with other tools keeps their files.
+// files this tuner writes (gemm_*.json, tile_ir_*.json) and then the directory
+// if it is empty, so a directory shared with other tools keeps their files.
 int t0g_tuner_clear(t0g_tuner *tuner) {
     if (!tuner) return fail(T0G_ERR_INVALID_ARG, "tuner is NULL");
     std::lock_guard<std::mutex> lk(tuner->mu);
@@ -629,8 +667,8 @@ int t0g_tuner_clear(t0g_tuner *tuner) {
         std::vector<std::string> victims;
         while (struct dirent *de = readdir(d)) {
             const std::string name = de->d_name;
-            if (name.compare(0, 5, "gemm_") == 0 && name.size() > 5 &&
-                name.compare(name.size() - 5, 5, ".json") == 0)
+            const bool ours = name.compare(0, 5, "gemm_") == 0 || name.compare(0, 8, "tile_ir_") == 0;
+            if (ours && name.size() > 8 && name.compare(name.size() - 5, 5, ".json") == 0)
                 victims.push_back(tuner->dir + "/" + name);
         }
         closedir(d);
@@ -648,9 +686,9 @@ int t0g_tuner_report(t0g_tuner *tuner, char *buf, size_t len, size_t *needed) {
     for (const auto &kv : tuner->cache) {
         const TuneKey &k = kv.first;
         const t0g_tune_result &r = kv.second.result;
-        snprintf(line, sizeof line, "  %ux%ux%u %s %s -> %s (%.1f TF) %s\n", k.m, k.n, k.k, kLayoutTag[k.transpose],
-                 k.out_dtype == T0G_BF16 ? "bf16" : "f32", config_name(r.best).c_str(), r.best_tflops,
-                 r.from_cache ? "[cached]" : "[measured]");
+        snprintf(line, sizeof line, "  %s%ux%ux%u %s %s -> %s (%.1f TF) %s\n", k.kind == kTileIr ? "tile_ir " : "",
+                 k.m, k.n, k.k, kLayoutTag[k.transpose], k.out_dtype == T0G_BF16 ? "bf16" : "f32",
+                 entry_name(k, r.best).c_str(), r.best_tflops, r.from_cache ? "[cached]" : "[measured]");
         s += line;
     }
     *needed = s.size() + 1;
@@ -659,6 +697,79 @@ int t0g_tuner_report(t0g_tuner *tuner, char *buf, size_t len, size_t *needed) {
         memcpy(buf, s.data(), n);
         buf[n] = 0;
     }
+    return ok();
+}
+
+static TuneKey tile_key(uint32_t m, uint32_t n, uint32_t k) {
+    TuneKey key{m, n, k, T0G_NT, T0G_F32};
+    key.kind = kTileIr;
+    return key;
+}
+
+int t0g_tune_tile_ir(t0g_tuner *tuner, t0g_device *dev, uint32_t m, uint32_t n, uint32_t k, t0g_tune_result *out) {
+    if (!dev || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (!tuner) {
+        int rc = t0g_tuner_global(&tuner);
+        if (rc) return rc;
+    }
+    if (int rc = check_key(m, n, k, T0G_NT, T0G_F32)) return rc;
+    std::lock_guard<std::mutex> lk(tuner->mu);
+    const TuneEntry *e = nullptr;
+    if (int rc = tune_locked(tuner, dev, tile_key(m, n, k), &e)) return rc;
+    *out = e->result;
+    return ok();
+}
+
+int t0g_tile_ir_lookup(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, t0g_tune_result *out, int *found) {
+    if (!tuner || !out || !found) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = check_key(m, n, k, T0G_NT, T0G_F32)) return rc;
+    std::lock_guard<std::mutex> lk(tuner->mu);
+    const TuneEntry *e = find_entry(tuner, tile_key(m, n, k));
+    *found = e != nullptr;
+    if (e) *out = e->result;
+    return ok();
+}
+
+int t0g_tile_ir_ranking(t0g_tuner *tuner, uint32_t m, uint32_t n, uint32_t k, uint32_t i, char *name, size_t name_len,
+                        double *tflops) {
+    if (!tuner || !name || name_len == 0 || !tflops) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (int rc = check_key(m, n, k, T0G_NT, T0G_F32)) return rc;
+    std::lock_guard<std::mutex> lk(tuner->mu);
+    const TuneEntry *e = find_entry(tuner, tile_key(m, n, k));
+    if (!e) return fail(T0G_ERR_INVALID_ARG, "no tile_ir tuning result for %ux%ux%u", m, n, k);
+    if (i >= e->all.size()) return fail(T0G_ERR_INVALID_ARG, "ranking index %u >= %zu", i, e->all.size());
+    const std::string &s = e->all[i].first;
+    if (s.size() + 1 > name_len) return fail(T0G_ERR_INVALID_ARG, "name buffer too small");
+    memcpy(name, s.c_str(), s.size() + 1);
+    *tflops = e->all[i].second;
+    return ok();
+}
+
+int t0g_tile_ir_store(t0g_tuner *tuner, const t0g_tune_result *result, const char *const *names, const double *tflops,
+                      uint32_t n_all) {
+    if (!tuner || !result || (n_all && (!names || !tflops))) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    const TuneKey key = tile_key(result->m, result->n, result->k);
+    if (int rc = check_key(key.m, key.n, key.k, key.transpose, key.out_dtype)) return rc;
+    t0g_gemm_config cfg = result->best;
+    cfg.transpose = T0G_NT;
+    if (int rc = validate(&cfg)) return rc;
+    if (cfg.split_k == T0G_STREAM_K) return fail(T0G_ERR_UNSUPPORTED_CONFIG, "the tile ABI has no stream-K launch");
+    TuneEntry e;
+    e.result = *result;
+    e.result.best = cfg;
+    e.result.transpose = T0G_NT;
+    e.result.out_dtype = T0G_F32;
+    e.result.from_cache = 0;
+    for (uint32_t i = 0; i < n_all; ++i) {
+        if (!names[i]) return fail(T0G_ERR_INVALID_ARG, "names[%u] is NULL", i);
+        if (strchr(names[i], '"') || strchr(names[i], '\\'))
+            return fail(T0G_ERR_INVALID_ARG, "names[%u] contains a quote or backslash", i);
+        e.all.emplace_back(names[i], tflops[i]);
+    }
+    e.result.n_all = n_all;
+    std::lock_guard<std::mutex> lk(tuner->mu);
+    if (int rc = save_entry(tuner, key, e)) return rc;
+    tuner->cache[key] = std::move(e);
     return ok();
 }
 

@@ -134,6 +134,54 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class KernelMeta(ctypes.Structure):
+    """A kernel's entry in a gfx950 code object's AMDGPU metadata (t0g_kernel_meta)."""
+
+    _fields_ = [
+        ("kernarg_size", ctypes.c_uint32),
+        ("kernarg_segment_size", ctypes.c_uint32),
+        ("group_segment_size", ctypes.c_uint32),
+        ("private_segment_size", ctypes.c_uint32),
+        ("max_workgroup_size", ctypes.c_uint32),
+        ("wavefront_size", ctypes.c_uint32),
+    ]
+
+
+class CompiledKernel(ctypes.Structure):
+    """T0Kernel::compile output for a problem (t0g_compiled_kernel): code object,
+    symbol, launch shape and argument block."""
+
+    _fields_ = [
+        ("code_object", ctypes.c_void_p),
+        ("code_object_size", ctypes.c_size_t),
+        ("name", ctypes.c_char * 96),
+        ("workgroup_size", ctypes.c_uint32),
+        ("lds_size", ctypes.c_uint32),
+        ("kernarg_size", ctypes.c_uint32),
+        ("grid", ctypes.c_uint32 * 3),
+        ("splits", ctypes.c_uint32),
+        ("kernargs", ctypes.c_uint8 * 160),
+    ]
+
+    def elf(self):
+        """The code object's bytes (CompiledKernel.elf)."""
+        return ctypes.string_at(self.code_object, self.code_object_size)
+
+    def args(self):
+        return bytes(self.kernargs[:self.kernarg_size])
+
+
+class PoolInfo(ctypes.Structure):
+    _fields_ = [
+        ("cached_bytes", ctypes.c_uint64),
+        ("cached_buffers", ctypes.c_uint64),
+        ("live_bytes", ctypes.c_uint64),
+        ("live_buffers", ctypes.c_uint64),
+        ("hits", ctypes.c_uint64),
+        ("misses", ctypes.c_uint64),
+    ]
+
+
 _u32 = ctypes.c_uint32
 _u64 = ctypes.c_uint64
 _p = ctypes.c_void_p
@@ -155,6 +203,8 @@ _sig("t0g_config_validate", ctypes.c_int, _cfgp)
 _sig("t0g_config_n_waves", _u32, _cfgp)
 _sig("t0g_config_lds_total", _u32, _cfgp)
 _sig("t0g_config_name", ctypes.c_int, _cfgp, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_tile_config_name", ctypes.c_int, _cfgp, _u32, ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_code_object_kernel_meta", ctypes.c_int, _p, ctypes.c_size_t, ctypes.c_char_p, ctypes.POINTER(KernelMeta))
 _sig("t0g_auto_select", ctypes.c_int, _u32, _u32, _u32, _cfgp)
 _sig("t0g_tile_auto_select", ctypes.c_int, _u32, _u32, _u32, _u32, _cfgp)
 _sig("t0g_compute_grid", ctypes.c_int, _cfgp, _u32, _u32, _u32p, _u32p)
@@ -186,6 +236,13 @@ _sig("t0g_device_is_poisoned", ctypes.c_int, _p, ctypes.POINTER(ctypes.c_int))
 _sig("t0g_alloc", ctypes.c_int, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
 _sig("t0g_alloc_zero", ctypes.c_int, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
 _sig("t0g_free", ctypes.c_int, _p, _u64)
+_sig("t0g_recycle", ctypes.c_int, _p, _u64)
+_sig("t0g_pool_clear", ctypes.c_int, _p)
+_sig("t0g_pool_stats", ctypes.c_int, _p, ctypes.POINTER(PoolInfo))
+_sig("t0g_alloc_f32", ctypes.c_int, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
+_sig("t0g_write_f32", ctypes.c_int, _p, _u64, _p, ctypes.c_size_t)
+_sig("t0g_read_f32", ctypes.c_int, _p, _u64, _p, ctypes.c_size_t)
+_sig("t0g_upload_f32", ctypes.c_int, _p, _p, ctypes.c_size_t, ctypes.POINTER(_u64))
 _sig("t0g_memcpy_h2d", ctypes.c_int, _p, _u64, _p, ctypes.c_size_t)
 _sig("t0g_memcpy_d2h", ctypes.c_int, _p, _p, _u64, ctypes.c_size_t)
 _sig("t0g_memset", ctypes.c_int, _p, _u64, ctypes.c_int, ctypes.c_size_t)
@@ -202,6 +259,7 @@ _sig("t0g_gemm", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
 _sig("t0g_gemm_workspace_size", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_gemm_group", ctypes.c_int, _p, ctypes.POINTER(GemmDesc), _u32)
 _sig("t0g_gemm_kernel_name", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_size_t)
+_sig("t0g_gemm_compile", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(CompiledKernel))
 _sig("t0g_f32_to_bf16", ctypes.c_int, _p, _u64, _u64, ctypes.c_size_t)
 _sig("t0g_matmul_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_backward_data_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
@@ -245,11 +303,19 @@ _sig("t0g_tuner_invalidate", ctypes.c_int, _p, _u32, _u32, _u32, _u32, _u32)
 _sig("t0g_tuner_clear", ctypes.c_int, _p)
 _sig("t0g_tuner_report", ctypes.c_int, _p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_auto_gemm", ctypes.c_int, _p, _p, _u64, _u64, _u64, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_double))
+_sig("t0g_tune_tile_ir", ctypes.c_int, _p, _p, _u32, _u32, _u32, ctypes.POINTER(TuneResult))
+_sig("t0g_tile_ir_lookup", ctypes.c_int, _p, _u32, _u32, _u32, ctypes.POINTER(TuneResult), ctypes.POINTER(ctypes.c_int))
+_sig("t0g_tile_ir_ranking", ctypes.c_int, _p, _u32, _u32, _u32, _u32, ctypes.c_char_p, ctypes.c_size_t,
+     ctypes.POINTER(ctypes.c_double))
+_sig("t0g_tile_ir_store", ctypes.c_int, _p, ctypes.POINTER(TuneResult), ctypes.POINTER(ctypes.c_char_p),
+     ctypes.POINTER(ctypes.c_double), _u32)
 _sig("t0g_stream_k_begin", _u32, _u32, _u32, _u32)
 _sig("t0g_stream_k_worker", _u32, _u32, _u32, _u32)
 _sig("t0g_stream_k_timeouts", ctypes.c_int, _p, _u32p)
 _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
+_sig("t0g_set_stream_k_spin_limit", ctypes.c_int, _u32)
+_sig("t0g_debug_stream_k_stall", ctypes.c_int, ctypes.c_int)
 
 
 def _check(rc):
@@ -414,6 +480,37 @@ def gemm_kernel_name(desc):
     return buf.value.decode()
 
 
+def gemm_compile(desc):
+    """T0Kernel::compile + build_kernargs + compute_grid for desc (host only)."""
+    out = CompiledKernel()
+    _check(_lib.t0g_gemm_compile(ctypes.byref(desc), ctypes.byref(out)))
+    return out
+
+
+def code_object_kernel_meta(code_object, symbol):
+    """KernelMeta of `symbol` in a gfx950 code object (bytes), read on the host."""
+    blob = bytes(code_object)
+    buf = ctypes.create_string_buffer(blob, len(blob))
+    meta = KernelMeta()
+    _check(_lib.t0g_code_object_kernel_meta(buf, len(blob), symbol.encode(), ctypes.byref(meta)))
+    return meta
+
+
+def tile_config_name(cfg, chain=0):
+    """TileGemm::name (src/t0/tile_ir.rs:398-430)."""
+    buf = ctypes.create_string_buffer(160)
+    _check(_lib.t0g_tile_config_name(ctypes.byref(cfg), chain, buf, len(buf)))
+    return buf.value.decode()
+
+
+def set_stream_k_spin_limit(polls):
+    _check(_lib.t0g_set_stream_k_spin_limit(polls))
+
+
+def debug_stream_k_stall(on):
+    _check(_lib.t0g_debug_stream_k_stall(1 if on else 0))
+
+
 def debug_fail_hip_call(n):
     _check(_lib.t0g_debug_fail_hip_call(n))
 
@@ -496,6 +593,44 @@ class GpuRuntime:
 
     def free(self, addr):
         _check(_lib.t0g_free(self.handle, addr))
+
+    def recycle(self, addr):
+        """GpuRuntime::recycle: back to the buffer pool instead of freed."""
+        _check(_lib.t0g_recycle(self.handle, addr))
+
+    def pool_clear(self):
+        _check(_lib.t0g_pool_clear(self.handle))
+
+    def pool_stats(self):
+        info = PoolInfo()
+        _check(_lib.t0g_pool_stats(self.handle, ctypes.byref(info)))
+        return {f: getattr(info, f) for f, _ in PoolInfo._fields_}
+
+    def alloc_f32(self, n):
+        """GpuRuntime::alloc_f32: n floats, 512-byte padded, zeroed."""
+        a = ctypes.c_uint64()
+        _check(_lib.t0g_alloc_f32(self.handle, n, ctypes.byref(a)))
+        return a.value
+
+    def write_f32(self, addr, data):
+        import numpy as np
+        arr = np.ascontiguousarray(data, dtype=np.float32)
+        _check(_lib.t0g_write_f32(self.handle, addr, arr.ctypes.data, arr.size))
+
+    def read_f32(self, addr, n):
+        """GpuRuntime::read_f32: waits for queued work, then copies n floats."""
+        import numpy as np
+        out = np.empty(n, dtype=np.float32)
+        _check(_lib.t0g_read_f32(self.handle, addr, out.ctypes.data, n))
+        return out
+
+    def upload_f32(self, data):
+        """GpuRuntime::upload_f32: alloc_f32 + write_f32."""
+        import numpy as np
+        arr = np.ascontiguousarray(data, dtype=np.float32)
+        a = ctypes.c_uint64()
+        _check(_lib.t0g_upload_f32(self.handle, arr.ctypes.data, arr.size, ctypes.byref(a)))
+        return a.value
 
     def write(self, addr, array):
         """Host numpy array -> device (GpuBuffer::write)."""
@@ -719,6 +854,41 @@ class GemmTuner:
     def clear(self):
         _check(_lib.t0g_tuner_clear(self.handle))
 
+    def tune_tile_ir(self, rt, m, n, k):
+        """tune_tile_ir(rt, m, n, k) (src/t0/cost_model.rs:788-1013) -> TuneResult."""
+        r = TuneResult()
+        _check(_lib.t0g_tune_tile_ir(self.handle, rt.handle, m, n, k, ctypes.byref(r)))
+        return r
+
+    def tile_ir_lookup(self, m, n, k):
+        r = TuneResult()
+        found = ctypes.c_int()
+        _check(_lib.t0g_tile_ir_lookup(self.handle, m, n, k, ctypes.byref(r), ctypes.byref(found)))
+        return r if found.value else None
+
+    def tile_ir_ranking(self, m, n, k):
+        """TileIrTuneResult::all: [(TileGemm name, TFLOPS)], fastest first."""
+        r = self.tile_ir_lookup(m, n, k)
+        if r is None:
+            return []
+        out = []
+        buf = ctypes.create_string_buffer(256)
+        tf = ctypes.c_double()
+        for i in range(r.n_all):
+            _check(_lib.t0g_tile_ir_ranking(self.handle, m, n, k, i, buf, len(buf), ctypes.byref(tf)))
+            out.append((buf.value.decode(), tf.value))
+        return out
+
+    def save_tile_ir_cache(self, m, n, k, best, best_tflops, all_=()):
+        """save_tile_ir_cache (src/t0/cost_model.rs:1076-1093)."""
+        r = TuneResult()
+        r.best = best
+        r.best_tflops = best_tflops
+        r.m, r.n, r.k = m, n, k
+        names = (ctypes.c_char_p * max(1, len(all_)))(*[nm.encode() for nm, _ in all_])
+        tfs = (ctypes.c_double * max(1, len(all_)))(*[t for _, t in all_])
+        _check(_lib.t0g_tile_ir_store(self.handle, ctypes.byref(r), names, tfs, len(all_)))
+
     def report(self):
         need = ctypes.c_size_t()
         _check(_lib.t0g_tuner_report(self.handle, None, 0, ctypes.byref(need)))
@@ -733,6 +903,14 @@ def auto_gemm(rt, a, b, c, m, n, k, tuner=None):
     tf = ctypes.c_double()
     _check(_lib.t0g_auto_gemm(tuner.handle if tuner is not None else None, rt.handle, a, b, c, m, n, k, ctypes.byref(tf)))
     return tf.value
+
+
+def tune_tile_ir(rt, m, n, k, tuner=None):
+    """tune_tile_ir(rt, m, n, k) -> TileIrTuneResult (src/t0/cost_model.rs:788-1013),
+    on the global tuner unless one is given."""
+    r = TuneResult()
+    _check(_lib.t0g_tune_tile_ir(tuner.handle if tuner is not None else None, rt.handle, m, n, k, ctypes.byref(r)))
+    return r
 
 
 def stream_k_begin(total, grid, w):

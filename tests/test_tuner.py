@@ -160,9 +160,10 @@ def test_invalidate_and_clear(tmp_path):
         assert len(t) == 0
         assert not (tmp_path / "cache").exists()
         t.save_cache(512, 512, 512, cfg, 2.0)
-        _write(tmp_path, "tile_ir_1x1x1.json", "{}")
+        t.save_tile_ir_cache(512, 512, 512, cfg, 2.0)
+        _write(tmp_path, "notes.json", "{}")
         t.clear()
-        assert os.listdir(tmp_path / "cache") == ["tile_ir_1x1x1.json"]
+        assert os.listdir(tmp_path / "cache") == ["notes.json"]   # gemm_* and tile_ir_* are this tuner's
 
 
 def test_store_rejects_bad_input(tmp_path):
@@ -212,3 +213,66 @@ def test_candidates_cover_every_tile():
     cands = t0g.tune_candidates(4096, 4096, 4096, "NT", 64)
     assert {(c.tile_m, c.tile_n) for c in cands} == {(256, 256), (128, 128), (64, 64)}
     assert len(cands) == 3 * 5 + 1   # 3 tiles x split 1..16 (64 K tiles, >= 4 per split), and stream-K
+
+
+# ---- tune_tile_ir's cache (src/t0/cost_model.rs:1030-1097) ----------------------
+
+def test_tile_ir_cache_roundtrip(tmp_path):
+    """save_tile_ir_cache then load_tile_ir_cache on a new tuner: the same tile, split
+    and TFLOPS, from_cache, the TileGemm-named ranking (cost_model.rs:1076-1093)."""
+    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=8)
+    ranking = [(t0g.tile_config_name(cfg), 271.3), ("tile_gemm_64x64_k64_db_sk2", 200.0)]
+    with _tuner(tmp_path) as t:
+        t.save_tile_ir_cache(128, 4096, 4096, cfg, 271.3, ranking)
+        assert t.tile_ir_lookup(128, 4096, 4096).from_cache == 0
+        assert t.lookup(128, 4096, 4096) is None          # a separate cache from GemmTuner's
+    js = json.loads((tmp_path / "cache" / "tile_ir_128x4096x4096.json").read_text())
+    for key in ("tile_m", "tile_n", "tile_k", "split_k", "wgp", "tflops", "all"):   # the reference's keys
+        assert key in js, key
+    assert (js["tile_m"], js["tile_n"], js["tile_k"], js["split_k"], js["wgp"]) == (128, 128, 64, 8, False)
+    assert js["arch"] == "gfx950"
+    with _tuner(tmp_path) as t2:
+        r = t2.tile_ir_lookup(128, 4096, 4096)
+        assert r is not None and r.from_cache == 1
+        assert (r.best.tile_m, r.best.tile_n, r.best.split_k, r.best.wg_size) == (128, 128, 8, 256)
+        assert r.best.transpose == t0g.NT and abs(r.best_tflops - 271.3) < 0.01
+        assert t2.tile_ir_ranking(128, 4096, 4096) == [(n, pytest.approx(v, abs=0.01)) for n, v in ranking]
+        assert "tile_ir 128x4096x4096" in t2.report()
+
+
+def test_tile_ir_file_of_the_gfx1100_build_is_a_miss(tmp_path):
+    """The file save_tile_ir_cache writes on gfx1100 (no arch; an RDNA3 tile) is re-tuned here."""
+    _write(tmp_path, "tile_ir_4096x4096x4096.json",
+           '{"tile_m":128,"tile_n":128,"tile_k":32,"split_k":1,"wgp":false,"tflops":84.70,'
+           '"all":[["tile_gemm_128x128_k32_db",84.70]]}')
+    with _tuner(tmp_path) as t:
+        assert t.tile_ir_lookup(4096, 4096, 4096) is None
+
+
+def test_tile_ir_file_without_wg_size_loads(tmp_path):
+    """load_tile_ir_cache reads no workgroup size (cost_model.rs:1059-1074): the tile gives it."""
+    _write(tmp_path, "tile_ir_256x256x32768.json",
+           '{"tile_m":64,"tile_n":64,"tile_k":64,"split_k":16,"wgp":false,"tflops":243.1,"arch":"gfx950"}')
+    with _tuner(tmp_path) as t:
+        r = t.tile_ir_lookup(256, 256, 32768)
+        assert r is not None and (r.best.wg_size, r.best.split_k) == (256, 16)
+        assert t0g.tile_config_name(r.best) == "tile_gemm_64x64_k64_db_sk16"
+
+
+@pytest.mark.parametrize("text", [
+    '{"tile_m":256,"tile_n":256,"tile_k":64,"split_k":2147483648,"wgp":false,"tflops":1,"arch":"gfx950"}',
+    '{"tile_m":96,"tile_n":64,"tile_k":64,"split_k":1,"wgp":false,"tflops":1,"arch":"gfx950"}',
+    '{"tile_m":64,"tile_n":64,"tile_k":64,"split_k":1,"wgp":false,"arch":"gfx950"}',
+])
+def test_tile_ir_bad_files_are_misses(tmp_path, text):
+    _write(tmp_path, "tile_ir_64x64x64.json", text)
+    with _tuner(tmp_path) as t:
+        assert t.tile_ir_lookup(64, 64, 64) is None
+
+
+def test_tile_ir_store_refuses_stream_k(tmp_path):
+    with _tuner(tmp_path) as t:
+        sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+        with pytest.raises(t0g.T0gError) as e:
+            t.save_tile_ir_cache(4352, 4096, 8192, sk, 1.0)
+        assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG
