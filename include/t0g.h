@@ -333,6 +333,18 @@ typedef struct t0g_gemm_desc {
 /* Enqueue C = op(A) * op(B) (+ epilogue) on the device stream (asynchronous).
  * split_k > 1: fp32 partial planes, then a deterministic plane-ordered reduce. */
 T0G_API int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *desc);
+/* t0g_gemm without allocating (no reference counterpart: for callers that cannot
+ * allocate device memory, such as code under HIP graph capture, tight serving
+ * loops or harnesses that forbid hipMalloc).  Same arguments and results as
+ * t0g_gemm; the fp32 split-K planes go to desc->workspace if given, else to a
+ * static per-device scratch array of T0G_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends (a problem needing more
+ * returns T0G_ERR_INVALID_ARG).  Stream-K configs run the data-parallel schedule
+ * of the same tile.  Every call on one GPU shares that GPU's scratch, which keeps
+ * the last call's partial sums: calls in the same stream are ordered, but calls
+ * that overlap on one GPU (other streams or device handles) race on it. */
+#define T0G_NOALLOC_SCRATCH_BYTES (64u << 20)
+T0G_API int t0g_gemm_noalloc(t0g_device *dev, const t0g_gemm_desc *desc);
 /* Enqueue n GEMMs that do not depend on each other (no output of one is an
  * input or output of another) to run concurrently: round-robin over the device
  * stream and two side streams forked from it (default priority, each with its

@@ -68,6 +68,10 @@ struct KernelMeta {
 // offload bundle); refuses objects for other GPUs and malformed input.
 int read_kernel_meta(const void *code_object, size_t size, const char *symbol, KernelMeta *out);
 
+// Device address of device `ordinal`'s copy of the no-allocation scratch array
+// (t0g_noalloc.hip); the device must be current on the first call for it.
+int noalloc_scratch(int ordinal, uint64_t *ptr);
+
 }  // namespace t0g
 
 #endif

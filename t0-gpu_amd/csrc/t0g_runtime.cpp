@@ -79,6 +79,8 @@ struct t0g_device {
     uint64_t conv = 0;         // bf16 operand scratch of the matmul entry points
     size_t conv_bytes = 0;
     uint32_t num_cus = 0;      // compute units: the stream-K grid
+    uint64_t scratch = 0;      // this device's no-allocation scratch (0: unavailable, see scratch_error)
+    std::string scratch_error;
     uint64_t sk_sync = 0;      // stream-K control words and ready flags (zero between launches)
     hipStream_t sk_stream = nullptr;   // stream of a stream-K launch whose timeout word is not yet checked
     // t0g_gemm_group: side streams (default priority), each with its own split-K
@@ -591,6 +593,12 @@ int t0g_device_open(int ordinal, t0g_device **out) {
     if ((e = T0G_HIP(hipStreamCreateWithFlags(&dev->own_stream, hipStreamNonBlocking))) != hipSuccess)
         return hip_fail(e, "hipStreamCreate");
     dev->stream = dev->own_stream;
+    // set-up of t0g_gemm_noalloc's scratch, with this device current; a failure
+    // only disables that entry point
+    if (noalloc_scratch(ordinal, &dev->scratch) != T0G_OK) {
+        dev->scratch = 0;
+        dev->scratch_error = g_last_error;
+    }
     if ((e = T0G_HIP(hipModuleLoadData(&dev->module, t0g_hsaco_begin))) != hipSuccess) {
         (void)hipStreamDestroy(dev->own_stream);
         return hip_fail(e, "hipModuleLoadData(gfx950 GEMM code object)");
@@ -1202,6 +1210,52 @@ int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *d) {
     if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
     std::lock_guard<std::mutex> lk(dev->mu);
     return gemm_locked(dev, d);
+}
+
+// t0g_gemm without allocating: the split-K planes go to the caller's workspace or
+// to the device's static scratch array; stream-K configs take the data-parallel
+// schedule of the same tile (their flag words would be allocated).  No hipMalloc,
+// hipFree or other allocating call is made here.
+int t0g_gemm_noalloc(t0g_device *dev, const t0g_gemm_desc *d) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (!dev->scratch)
+        return fail(T0G_ERR_HIP, "no-allocation scratch unavailable on device %d: %s", dev->ordinal,
+                    dev->scratch_error.c_str());
+    t0g_gemm_config cfg;
+    GemmPlan p;
+    GemmOperands o;
+    int rc = resolve_desc(d, &cfg, &p, &o);
+    if (rc) return rc;
+    if (p.stream_k) {
+        t0g_gemm_config dp = cfg;
+        dp.split_k = 0;
+        t0g_gemm_desc d2 = *d;
+        d2.config = &dp;
+        d2.split_k = 1;
+        if ((rc = resolve_desc(&d2, &cfg, &p, &o))) return rc;
+    }
+    if ((rc = check_usable(dev))) return rc;
+    if (d->m == 0 || d->n == 0) return ok();
+    uint64_t ws = 0;
+    if (p.splits > 1) {
+        const size_t need = (size_t)p.splits * d->m * d->n * 4;
+        if (d->workspace) {
+            if (d->workspace_bytes < need)
+                return fail(T0G_ERR_INVALID_ARG, "workspace of %llu bytes, split-K needs %zu",
+                            (unsigned long long)d->workspace_bytes, need);
+            ws = d->workspace;
+        } else {
+            if (need > (size_t)T0G_NOALLOC_SCRATCH_BYTES)
+                return fail(T0G_ERR_INVALID_ARG,
+                            "split-K of %ux%u over %u planes needs %zu bytes of scratch; t0g_gemm_noalloc has %u "
+                            "(ask for fewer splits with desc.split_k, or pass a workspace)",
+                            d->m, d->n, p.splits, need, (unsigned)T0G_NOALLOC_SCRATCH_BYTES);
+            ws = dev->scratch;
+        }
+    }
+    if ((rc = run_plan(dev, p, o, ws))) return rc;
+    return ok();
 }
 
 // Independent GEMMs, round-robin over the device stream and the side streams.

@@ -258,6 +258,7 @@ _sig("t0g_wait_idle", ctypes.c_int, _p)
 _sig("t0g_gemm", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
 _sig("t0g_gemm_workspace_size", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_size_t))
 _sig("t0g_gemm_group", ctypes.c_int, _p, ctypes.POINTER(GemmDesc), _u32)
+_sig("t0g_gemm_noalloc", ctypes.c_int, _p, ctypes.POINTER(GemmDesc))
 _sig("t0g_gemm_kernel_name", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_size_t)
 _sig("t0g_gemm_compile", ctypes.c_int, ctypes.POINTER(GemmDesc), ctypes.POINTER(CompiledKernel))
 _sig("t0g_f32_to_bf16", ctypes.c_int, _p, _u64, _u64, ctypes.c_size_t)
@@ -695,6 +696,11 @@ class GpuRuntime:
 
     def gemm_desc(self, desc):
         _check(_lib.t0g_gemm(self.handle, ctypes.byref(desc)))
+
+    def gemm_noalloc(self, desc):
+        """t0g_gemm without allocating: split-K planes in the device's static scratch
+        array (T0G_NOALLOC_SCRATCH_BYTES) or desc.workspace."""
+        _check(_lib.t0g_gemm_noalloc(self.handle, ctypes.byref(desc)))
 
     def gemm_group(self, descs):
         """Enqueue independent GEMMs (GemmDesc list) to run concurrently."""
