@@ -425,7 +425,8 @@ def main():
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
                     help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
                          "COPY:MiB instead times a plain device-to-device copy of that size, the "
-                         "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters")
+                         "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters; MLP or "
+                         "MLP_GROUPED times benchmark config 5's step (six GEMMs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures the GEMM on one GPU only "
@@ -472,6 +473,14 @@ def main():
         print(json.dumps({"only": args.only, "kernel": "t0g_f32_to_bf16_rne", "elements": n_el,
                           "us_per_launch": round(ms * 1e3, 2), "gbs": round(6.0 * n_el / (ms * 1e-3) / 1e9, 1)}),
               flush=True)
+        rt.set_stream(None)
+        rt.close()
+        return
+
+    if args.only and args.only.upper() in ("MLP", "MLP_GROUPED"):
+        r = mlp_step(t0g, torch, rt, stream, args.steps, args.warmup, grouped=args.only.upper() == "MLP_GROUPED")
+        print(json.dumps({"only": args.only, "ms_per_step": round(r["ms_per_step"], 5), "tflops": round(r["tflops"], 2),
+                          "frac_of_peak": round(r["frac_of_peak"], 4), "kernels": r["kernels"]}), flush=True)
         rt.set_stream(None)
         rt.close()
         return

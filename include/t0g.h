@@ -213,7 +213,10 @@ T0G_API int t0g_device_count(int *count);
  * selects the HIP device, creates its stream, loads the gfx950 code object. */
 T0G_API int t0g_device_open(int ordinal, t0g_device **out);
 T0G_API int t0g_device_close(t0g_device *dev);
-/* Run subsequent work on a caller-owned hipStream_t (NULL: back to the device's own). */
+/* Run subsequent work on a caller-owned hipStream_t (NULL: back to the device's own).
+ * On a change of stream the new stream first waits for the work issued on the
+ * old one (the handle's split-K workspace and control block are shared by all
+ * its launches, so they must not run at the same time). */
 T0G_API int t0g_device_set_stream(t0g_device *dev, void *hip_stream);
 T0G_API int t0g_device_get_stream(t0g_device *dev, void **hip_stream);
 T0G_API int t0g_device_is_poisoned(t0g_device *dev, int *poisoned);
@@ -331,7 +334,8 @@ typedef struct t0g_gemm_desc {
 } t0g_gemm_desc;
 
 /* Enqueue C = op(A) * op(B) (+ epilogue) on the device stream (asynchronous).
- * split_k > 1: fp32 partial planes, then a deterministic plane-ordered reduce. */
+ * split_k > 1: fp32 partial sums of each K slice, summed in plane order (by a
+ * reduce kernel, or inside the GEMM kernel: t0g_set_split_k_mode). */
 T0G_API int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *desc);
 /* t0g_gemm without allocating (no reference counterpart: for callers that cannot
  * allocate device memory, such as code under HIP graph capture, tight serving
@@ -516,8 +520,23 @@ T0G_API int t0g_stream_k_timeouts(t0g_device *dev, uint32_t *count);
 T0G_API int t0g_set_stream_k_spin_limit(uint32_t polls);
 /* on != 0: later stream-K launches wait on a control word nothing sets, so
  * every wait of a cut tile gives up at the spin limit and the kernels still
- * exit (a host-forced timeout for testing the error path); 0 restores. */
+ * exit (a host-forced timeout for testing the error path); 0 restores.  In a
+ * split-K launch reduced inside the kernel, the same switch makes every
+ * workgroup but a tile's last arrival give up waiting, so the last arrival
+ * sums the whole tile (the result does not change). */
 T0G_API int t0g_debug_stream_k_stall(int on);
+/* How t0g_gemm runs split-K (no reference counterpart; the reference sums the
+ * planes on the host): T0G_SPLIT_K_REDUCE_KERNEL (0, the default) = fp32 planes
+ * ([splits][M][N] in desc->workspace) plus the reduce kernel;
+ * T0G_SPLIT_K_IN_KERNEL (1) = reduced inside the GEMM kernel wherever the plan
+ * allows it (one launch; the K slices of a tile sum it in plane order), else as
+ * 0.  Both give the same bits.  The in-kernel form moves every partial through
+ * HBM twice while the tile's slices wait for each other; measured on MI355X it
+ * is slower than the two launches on the thin shapes and level on the MLP's,
+ * hence not the default.  Process-wide, for later calls. */
+#define T0G_SPLIT_K_REDUCE_KERNEL 0u
+#define T0G_SPLIT_K_IN_KERNEL 1u
+T0G_API int t0g_set_split_k_mode(uint32_t mode);
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
  * real device fault. */

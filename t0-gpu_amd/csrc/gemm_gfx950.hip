@@ -372,7 +372,9 @@ struct VecEpilogue {
     static constexpr uint32_t kWaveBytes = 32 * kStride;   // LDS per wave
 };
 
-template <int SM, int SN, bool OUT_BF16>
+// WT: the 16-byte stores write through to memory (sc0 sc1) instead of going
+// non-temporal into this XCD's L2, for data that workgroups on other XCDs read.
+template <int SM, int SN, bool OUT_BF16, bool WT = false>
 __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
                                                uint32_t col0, uint32_t lane, uint32_t lds, bool vec, uint32_t split) {
     typedef VecEpilogue<SN> E;
@@ -436,9 +438,12 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
 #pragma unroll
                     for (int c = 0; c < 4; ++c) w[c] = __builtin_bit_cast(uint32_t, v[c]);
                 }
-                // Non-temporal: C is not read again here, so keep it from
-                // evicting A/B panels that later tiles on this XCD still need.
-                __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
+                // Non-temporal (unless WT): C is not read again here, so keep it
+                // from evicting A/B panels that later tiles on this XCD still need.
+                if constexpr (WT)
+                    *reinterpret_cast<volatile __attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr) = w;
+                else
+                    __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
             } else if (grow < p.m) {
 #pragma unroll
                 for (int c = 0; c < kCols; ++c) {
@@ -963,14 +968,17 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
 
 }  // namespace t0g
 
+#include "gemm_red.h"
 #include "gemm_mfma16.h"
 
 namespace t0g {
 
 // Fast path: one BM x BN output tile per workgroup, operands streamed through
-// LDS by DMA (k_pipeline), epilogue staged through LDS.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS>
-__device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
+// LDS by DMA (k_pipeline), epilogue staged through LDS.  RED: split-K reduced
+// inside the kernel (ra: the launch's T0gGemmRedArgs, p = ra->g).
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS,
+          bool RED = false>
+__device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGemmRedArgs* ra = nullptr) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 32, SN = WTN / 32;
@@ -1032,9 +1040,24 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p) {
     static_assert((NT / 64) * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
     T0G_WAIT_VMCNT(0);    // LDS DMA still in flight (stages past K) has landed
     barrier_no_fence();   // and every wave is done with the ring
-    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
-    store_tile_vec<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                     lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec, gp.split);
+    if constexpr (RED) {
+        // the partial tile, raw fp32, row-major into this workgroup's slot
+        T0gGemmArgs q = p;
+        q.c = ra->partials + (uint64_t)(gp.tile * ra->splits + gp.split) * (BM * BN * 4u);
+        q.ldc = BN;
+        q.c_split_stride = 0;
+        q.epilogue = 0;
+        q.flags = T0G_FLAG_C_VEC;
+        store_tile_vec<SM, SN, false, true>(q, acc, wm * WTM, wn * WTN, lane,
+                                            lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, true, 0);
+        T0G_WAIT_VMCNT(0);    // the partial's stores have reached memory
+        barrier_no_fence();
+        red_finish<BM, BN, NT, OUT_BF16>(*ra, gp.tile, gp.split, m0, n0, lds_addr(smem), NS * STAGE);
+    } else {
+        const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+        store_tile_vec<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                         lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec, gp.split);
+    }
 }
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the
@@ -1293,6 +1316,36 @@ T0G_GEMM_LAYOUTS_256_X(bf16, true)
 T0G_GEMM_LAYOUTS_256_SK(f32, false)
 T0G_GEMM_LAYOUTS_256_SK(bf16, true)
 T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
+
+// Split-K reduced inside the kernel (suffix _r, T0gGemmRedArgs): 128x128 and
+// 256x256 tiles, every layout, f32 or bf16 out.
+#define T0G_GEMM_R(NAME, BM, BN, WM, WN, AK, BKM, OBF)                                                   \
+    extern "C" __global__ void __launch_bounds__(64 * WM * WN)                                           \
+        __attribute__((amdgpu_waves_per_eu(T0G_WPE_##BM##x##BN))) NAME(T0gGemmRedArgs ra) {              \
+        t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_##BM##x##BN, true>(ra.g, &ra);       \
+    }
+#define T0G_GEMM_LAYOUTS_R(PFX, BM, BN, WM, WN, OUTN, OBF)                 \
+    T0G_GEMM_R(PFX##_nt_##OUTN##_r, BM, BN, WM, WN, true, true, OBF)       \
+    T0G_GEMM_R(PFX##_nn_##OUTN##_r, BM, BN, WM, WN, true, false, OBF)      \
+    T0G_GEMM_R(PFX##_tn_##OUTN##_r, BM, BN, WM, WN, false, false, OBF)     \
+    T0G_GEMM_R(PFX##_tt_##OUTN##_r, BM, BN, WM, WN, false, true, OBF)
+T0G_GEMM_LAYOUTS_R(t0g_gemm_128x128_k64, 128, 128, 2, 2, f32, false)
+T0G_GEMM_LAYOUTS_R(t0g_gemm_128x128_k64, 128, 128, 2, 2, bf16, true)
+#define T0G_GEMM_256_R(NAME, AK, BKM, OBF)                                                                \
+    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
+        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmRedArgs ra) {            \
+        if constexpr (AK)                                                                                 \
+            t0g::gemm_tile_pp<AK, BKM, OBF, false, true>(ra.g, &ra);                                     \
+        else                                                                                              \
+            t0g::gemm_tile_fast16<AK, BKM, OBF, false, true>(ra.g, &ra);                                 \
+    }
+#define T0G_GEMM_LAYOUTS_256_R(OUTN, OBF)                                   \
+    T0G_GEMM_256_R(t0g_gemm_256x256_k64_nt_##OUTN##_r, true, true, OBF)     \
+    T0G_GEMM_256_R(t0g_gemm_256x256_k64_nn_##OUTN##_r, true, false, OBF)    \
+    T0G_GEMM_256_R(t0g_gemm_256x256_k64_tn_##OUTN##_r, false, false, OBF)   \
+    T0G_GEMM_256_R(t0g_gemm_256x256_k64_tt_##OUTN##_r, false, true, OBF)
+T0G_GEMM_LAYOUTS_256_R(f32, false)
+T0G_GEMM_LAYOUTS_256_R(bf16, true)
 T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_64x64_k64, 64, 64, 2, 2)

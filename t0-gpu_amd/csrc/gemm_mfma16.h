@@ -358,7 +358,8 @@ struct SkFixup {
     uint32_t frag;
 };
 
-template <int SM, int SN, bool OUT_BF16, bool FIXUP = false>
+// WT: 16-byte stores write through to memory (sc0 sc1), as in store_tile_vec.
+template <int SM, int SN, bool OUT_BF16, bool FIXUP = false, bool WT = false>
 __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32x4_t (&acc)[SM][SN], uint32_t row0,
                                                  uint32_t col0, uint32_t lane, uint32_t lds, bool vec,
                                                  SkFixup fx = SkFixup{0, 0, 0, 0}) {
@@ -449,7 +450,10 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
 #pragma unroll
                     for (int c = 0; c < 4; ++c) w[c] = __builtin_bit_cast(uint32_t, v[c]);
                 }
-                __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
+                if constexpr (WT)
+                    *reinterpret_cast<volatile __attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr) = w;
+                else
+                    __builtin_nontemporal_store(w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
             } else if (grow < p.m) {
 #pragma unroll
                 for (int c = 0; c < kCols; ++c) {
@@ -495,9 +499,33 @@ __device__ __forceinline__ void tile_origin(const T0gGemmArgs& p, uint32_t& m0, 
     n0 = (in_group / gsz) * BN;
 }
 
-// The 256x256 fast path on 16x16x32 MFMAs (2 x 2 waves of 128 x 128).
-template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false>
-__device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
+// Split-K reduced in the kernel, after the K loop of a 256x256 tile (16x16x32
+// result layout): the partial tile, raw fp32 and row-major, goes to this
+// workgroup's slot (tile blockIdx.x, split blockIdx.y) through the same
+// LDS-staged row stores as C (written through to memory), then the tile's
+// arrival, chunk sums and cleanup.
+template <int BM, int BN, int NT, int SM, int SN, bool OUT_BF16>
+__device__ __forceinline__ void red_store_and_finish(const T0gGemmArgs& p, const T0gGemmRedArgs& ra,
+                                                     const f32x4_t (&acc)[SM][SN], uint32_t row0, uint32_t col0,
+                                                     uint32_t lane, uint32_t wave, uint32_t m0, uint32_t n0,
+                                                     uint32_t lds, uint32_t lds_bytes) {
+    T0gGemmArgs q = p;
+    q.c = ra.partials + (uint64_t)(blockIdx.x * ra.splits + blockIdx.y) * (BM * BN * 4u);
+    q.ldc = BN;
+    q.c_split_stride = 0;
+    q.epilogue = 0;
+    q.flags = T0G_FLAG_C_VEC;
+    store_tile_vec16<SM, SN, false, false, true>(q, acc, row0, col0, lane, lds + wave * VecEpilogue16<SN>::kWaveBytes,
+                                                 true);
+    T0G_WAIT_VMCNT(0);    // the partial's stores have reached memory
+    barrier_no_fence();
+    red_finish<BM, BN, NT, OUT_BF16>(ra, blockIdx.x, blockIdx.y, m0, n0, lds, lds_bytes);
+}
+
+// The 256x256 fast path on 16x16x32 MFMAs (2 x 2 waves of 128 x 128).  RED:
+// split-K reduced inside the kernel (ra: the launch's T0gGemmRedArgs, p = ra->g).
+template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false, bool RED = false>
+__device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p, const T0gGemmRedArgs* ra = nullptr) {
     constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 2;
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -552,9 +580,14 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p) {
     mfma16_drain();
     T0G_WAIT_VMCNT(0);
     barrier_no_fence();
-    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
-    store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                       lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+    if constexpr (RED) {
+        red_store_and_finish<BM, BN, NT, SM, SN, OUT_BF16>(p, *ra, acc, wm * WTM, wn * WTN, lane, wave, m0, n0,
+                                                           lds_addr(smem), 2 * STAGE);
+    } else {
+        const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+        store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                           lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+    }
 }
 
 
@@ -632,9 +665,9 @@ __device__ __forceinline__ void k_pipeline_pp(f32x4_t (&acc)[SM][SN], const OpA&
 }
 
 // The 256x256 tile with 8 waves (2 x 4 of 128 x 64) in ping-pong: two waves per
-// SIMD, 128 accumulators each.
-template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false>
-__device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
+// SIMD, 128 accumulators each.  RED: split-K reduced inside the kernel.
+template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false, bool RED = false>
+__device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p, const T0gGemmRedArgs* ra = nullptr) {
     constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4;
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -687,9 +720,14 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p) {
     mfma16_drain();
     T0G_WAIT_VMCNT(0);
     barrier_no_fence();
-    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
-    store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                       lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+    if constexpr (RED) {
+        red_store_and_finish<BM, BN, NT, SM, SN, OUT_BF16>(p, *ra, acc, wm * WTM, wn * WTN, lane, wave, m0, n0,
+                                                           lds_addr(smem), 2 * STAGE);
+    } else {
+        const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+        store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                           lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
+    }
 }
 
 // ---- stream-K ------------------------------------------------------------------

@@ -45,6 +45,35 @@ typedef struct T0gGemmSkArgs {
     uint32_t reserved[2];    /* pads the block to 144 bytes (whole 16-byte words) */
 } T0gGemmSkArgs;
 
+/* Split-K with the reduction inside the GEMM kernel (suffix _r): the grid is
+ * tiles x splits as for plain split-K; each workgroup writes its fp32 partial
+ * tile (row-major [BM][BN]) to slot tile * splits + split of `partials`
+ * (stores written through to memory), then increments the tile's arrival
+ * counter.  The tile's result is summed in chunks (chunk c: elements
+ * [c E / splits, (c + 1) E / splits) of the row-major tile, E = BM * BN), each
+ * chunk by whichever workgroup claims it (sets its bit in the tile's claim
+ * mask first): the workgroup of split c, once the tile is complete, or the
+ * tile's last arrival for every chunk still unclaimed after its own.  Every
+ * chunk sums the splits in order 0, 1, ... from 0.0, the order of
+ * t0g_splitk_reduce, so the result does not depend on who summed it. */
+typedef struct T0gGemmRedArgs {
+    T0gGemmArgs g;           /* problem, operands, epilogue; c, ldc: the output  */
+    uint64_t partials;       /* f32 [tiles * splits][BM * BN]                    */
+    uint64_t sync;           /* u32: 16 control words, then one 128-byte line per
+                                tile: arrival counter, 64-bit claim mask (bit c:
+                                chunk c), done counter; all zero between launches */
+    uint32_t grid;           /* launched workgroups = tiles * splits              */
+    uint32_t splits;         /* K slices per tile: a power of two, 2 to 64        */
+    uint32_t spin_limit;     /* polls a helper waits for its tile to complete     */
+    uint32_t debug;          /* T0G_SK_DEBUG_* bits (0 in normal use)             */
+    uint32_t tiles;          /* output tiles = tiles_m * tiles_n                  */
+    uint32_t reserved;       /* pads the block to 144 bytes (whole 16-byte words) */
+} T0gGemmRedArgs;
+#define T0G_RED_ARRIVAL 16u      /* first tile line (after the control words)        */
+#define T0G_RED_LINE_WORDS 32u   /* words per tile line: counters of different tiles
+                                    never share a cache line                          */
+#define T0G_RED_MAX_GRID 16384u  /* workgroups of one fused split-K launch, at most  */
+
 #define T0G_SK_TILE 256u
 #define T0G_SK_SLOT_BYTES (T0G_SK_TILE * T0G_SK_TILE * 4u)
 #define T0G_SK_CTL_WORDS 16u

@@ -61,6 +61,7 @@ struct t0g_device {
     int ordinal = 0;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
+    hipEvent_t order_event = nullptr;   // orders launches across t0g_device_set_stream
     hipModule_t module = nullptr;
     std::mutex mu;
     bool poisoned = false;
@@ -102,6 +103,13 @@ static std::atomic<uint32_t> g_wait_timeout_ms{60000};
 // wait) before a workgroup gives up and counts a timeout.
 static std::atomic<uint32_t> g_sk_spin_limit{1u << 20};
 static std::atomic<uint32_t> g_sk_debug{0};
+// Split-K: 0 = reduce inside the GEMM kernel where the plan allows it (the _r
+// kernels), 1 = always partial planes plus the separate reduce kernel.
+static std::atomic<uint32_t> g_split_mode{T0G_SPLIT_K_REDUCE_KERNEL};
+// Polls a workgroup of a fused split-K launch waits for its tile's other K
+// slices before leaving its chunk to the tile's last arrival (a few tens of
+// microseconds: within one wave of workgroups the slices finish together).
+constexpr uint32_t kRedSpinLimit = 256;
 
 // Every HIP call goes through here so a test can make the n-th one fail.
 static bool injected_failure() {
@@ -222,6 +230,7 @@ struct GemmPlan {
     uint32_t wg;   // threads per workgroup of the chosen kernel
     bool stream_k;
     uint32_t sk_ipt;   // stream-K: 64-wide K steps per tile
+    bool fused;        // split-K reduced inside the GEMM kernel (_r symbol)
     std::string symbol;
 };
 
@@ -261,8 +270,10 @@ static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, 
     return OperandPath::Elementwise;
 }
 
+// allow_fused: the caller can run the in-kernel split-K reduction (its sync
+// words exist; not concurrent with another such launch of this device).
 static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, OperandPath path, uint32_t m,
-                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p) {
+                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p, bool allow_fused = false) {
     const bool aligned = path != OperandPath::Elementwise, wide = path == OperandPath::Wide;
     bool stream_k = split_req == T0G_STREAM_K;
     if (stream_k) split_req = 1;
@@ -291,6 +302,15 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     p->splits = sk;
     p->k_per_split = kps;
     const bool partial = sk > 1;
+    // In-kernel reduction: 128x128 and 256x256 tiles, a power-of-two split (the
+    // tile is summed in splits equal chunks), one wave of workgroups (a slice
+    // waits only for slices running at the same time) and slots addressable
+    // by a 32-bit buffer descriptor.
+    const uint64_t red_grid = (uint64_t)p->tiles_m * p->tiles_n * sk;
+    p->fused = partial && allow_fused && g_split_mode.load() == T0G_SPLIT_K_IN_KERNEL && aligned && !wide && !stream_k &&
+               (tile->bm == 256 || tile->bm == 128) && (sk & (sk - 1)) == 0 && sk <= kMaxSplitK &&
+               red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
+               red_grid * tile->bm * tile->bn * 4 < (1ull << 31);
     // At most one workgroup per CU: the 64x64 tile switches to its deep-ring
     // variant (the CU's LDS then holds one workgroup with 128 KB of stages;
     // measured 10 % faster on 256x256x32768 split 16, while 128x128 gained
@@ -302,8 +322,8 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     // faster.
     p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
-                ((out_bf16 && !partial) ? "bf16" : "f32") + (aligned ? (wide ? "_x" : deep ? "_d" : "") : "_u") +
-                (stream_k ? "_sk" : "");
+                ((out_bf16 && (!partial || p->fused)) ? "bf16" : "f32") +
+                (aligned ? (wide ? "_x" : deep ? "_d" : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
     if (stream_k && (uint64_t)p->tiles_m * p->tiles_n * p->sk_ipt > 0x7FFFFFFFull)
@@ -347,9 +367,13 @@ struct GemmOperands {
 
 // Stream-K control words and ready flags, allocated and zeroed once per device;
 // every launch leaves them zero again.
+// Also the control block of the in-kernel split-K reduction (arrival and claim
+// words after the control words); the two kinds of launch never overlap.
 static int ensure_sk_sync(t0g_device *dev) {
     if (dev->sk_sync) return T0G_OK;
-    const size_t bytes = (T0G_SK_CTL_WORDS + kNumCUs) * 4;
+    // a fused launch has at most T0G_RED_MAX_GRID / 2 tiles (two slices or more each)
+    const size_t bytes =
+        (T0G_SK_CTL_WORDS + std::max<size_t>(kNumCUs, (size_t)T0G_RED_LINE_WORDS * (T0G_RED_MAX_GRID / 2))) * 4;
     void *ptr = nullptr;
     hipError_t e = T0G_HIP(hipMalloc(&ptr, bytes));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(stream-K flags)");
@@ -380,7 +404,7 @@ static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws
     args.tiles_n = p.tiles_n;
     args.group_m = 8;
     args.flags = T0G_FLAG_XCD_REMAP;
-    const bool reduce = p.splits > 1 && o.c_split_stride == 0;
+    const bool reduce = p.splits > 1 && o.c_split_stride == 0 && !p.fused;
     if (reduce) {
         args.c = ws;
         args.ldc = o.n;
@@ -412,6 +436,20 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     T0gGemmArgs args;
     bool reduce = false;
     fill_gemm_args(p, o, ws, &args, &reduce);
+    if (p.fused) {
+        T0gGemmRedArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.g = args;
+        ra.partials = ws;
+        ra.sync = dev->sk_sync;
+        ra.tiles = p.tiles_m * p.tiles_n;
+        ra.grid = ra.tiles * p.splits;
+        ra.splits = p.splits;
+        ra.spin_limit = kRedSpinLimit;
+        ra.debug = g_sk_debug.load();
+        dev->sk_stream = dev->stream;
+        return launch(dev, f, p.tiles_m * p.tiles_n, p.splits, 1, p.wg, &ra, sizeof ra);
+    }
     if (p.stream_k) {
         T0gGemmSkArgs sa;
         memset(&sa, 0, sizeof sa);
@@ -466,7 +504,8 @@ static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, u
     return launch(dev, fr, (uint32_t)blocks, 1, 1, threads, &r, sizeof r);
 }
 
-static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *plan, GemmOperands *o) {
+static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *plan, GemmOperands *o,
+                        bool allow_fused = false) {
     if (!d) return fail(T0G_ERR_INVALID_ARG, "desc is NULL");
     if (d->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", d->transpose);
     if (d->out_dtype > T0G_BF16) return fail(T0G_ERR_INVALID_ARG, "bad out_dtype %u", d->out_dtype);
@@ -514,7 +553,16 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
         if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
         if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
     }
-    return make_plan(tile, t, d->out_dtype == T0G_BF16, path, d->m, d->n, d->k, sk, plan);
+    return make_plan(tile, t, d->out_dtype == T0G_BF16, path, d->m, d->n, d->k, sk, plan, allow_fused);
+}
+
+// Device workspace a plan needs: stream-K partial slots, fused split-K tile
+// slots, or split-K planes.
+static size_t plan_workspace(const GemmPlan &p, uint32_t m, uint32_t n, uint32_t num_cus) {
+    if (p.stream_k) return (size_t)sk_grid(p, num_cus) * T0G_SK_SLOT_BYTES;
+    if (p.fused) return (size_t)p.tiles_m * p.tiles_n * p.splits * p.tile->bm * p.tile->bn * 4;
+    if (p.splits > 1) return (size_t)p.splits * m * n * 4;
+    return 0;
 }
 
 }  // namespace t0g
@@ -556,6 +604,12 @@ int t0g_set_stream_k_spin_limit(uint32_t polls) {
 
 int t0g_debug_stream_k_stall(int on) {
     g_sk_debug.store(on ? T0G_SK_DEBUG_STALL : 0u);
+    return ok();
+}
+
+int t0g_set_split_k_mode(uint32_t mode) {
+    if (mode > 1) return fail(T0G_ERR_INVALID_ARG, "split-K mode %u (0: reduce kernel, 1: in-kernel reduce)", mode);
+    g_split_mode.store(mode);
     return ok();
 }
 
@@ -628,15 +682,33 @@ int t0g_device_close(t0g_device *dev) {
         for (uint64_t a : bucket.second) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
+    if (dev->order_event) (void)hipEventDestroy(dev->order_event);
     if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
     delete dev;
     return ok();
 }
 
+// The handle's split-K workspace and the control block of its stream-K and
+// in-kernel split-K launches are shared by everything it launches, so a
+// switch of stream makes the new stream wait for the work issued on the old
+// one: two launches of one handle never run at the same time.
 int t0g_device_set_stream(t0g_device *dev, void *hip_stream) {
     if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
     std::lock_guard<std::mutex> lk(dev->mu);
-    dev->stream = hip_stream ? (hipStream_t)hip_stream : dev->own_stream;
+    hipStream_t next = hip_stream ? (hipStream_t)hip_stream : dev->own_stream;
+    if (next != dev->stream) {
+        int rc = check_usable(dev);
+        if (rc) return rc;
+        hipError_t e = hipSuccess;
+        if (!dev->order_event &&
+            (e = T0G_HIP(hipEventCreateWithFlags(&dev->order_event, hipEventDisableTiming))) != hipSuccess)
+            return hip_fail(e, "hipEventCreateWithFlags");
+        if ((e = T0G_HIP(hipEventRecord(dev->order_event, dev->stream))) != hipSuccess)
+            return hip_fail(e, "hipEventRecord");
+        if ((e = T0G_HIP(hipStreamWaitEvent(next, dev->order_event, 0))) != hipSuccess)
+            return hip_fail(e, "hipStreamWaitEvent");
+    }
+    dev->stream = next;
     return ok();
 }
 
@@ -1023,7 +1095,7 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
         if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
     }
     GemmPlan p;
-    if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p))) return rc;
+    if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p, lib_planes))) return rc;
     if (p.tile != tile)   // another tile than the caller's grid was built for: refuse rather than re-grid
         return fail(T0G_ERR_UNSUPPORTED_CONFIG,
                     "tile %ux%u cannot take these operands (rows must be 16-byte aligned with K %% 8 == 0; "
@@ -1037,8 +1109,9 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
                         tiles_n, o.m, o.n, p.tiles_m, p.tiles_n);
         if (o.m == 0 || o.n == 0) return ok();
         uint64_t ws = 0;
+        if (p.fused && (rc = ensure_sk_sync(dev))) return rc;
         if (p.splits > 1) {
-            if ((rc = ensure_workspace(dev, (size_t)p.splits * o.m * o.n * 4))) return rc;
+            if ((rc = ensure_workspace(dev, plan_workspace(p, o.m, o.n, dev->num_cus)))) return rc;
             ws = dev->ws;
         }
         return run_plan(dev, p, o, ws);
@@ -1104,12 +1177,9 @@ int t0g_gemm_workspace_size(const t0g_gemm_desc *d, size_t *bytes) {
     t0g_gemm_config cfg;
     GemmPlan p;
     GemmOperands o;
-    int rc = resolve_desc(d, &cfg, &p, &o);
+    int rc = resolve_desc(d, &cfg, &p, &o, true);
     if (rc) return rc;
-    if (p.stream_k)
-        *bytes = (size_t)sk_grid(p, kNumCUs) * T0G_SK_SLOT_BYTES;
-    else
-        *bytes = p.splits > 1 ? (size_t)p.splits * d->m * d->n * 4 : 0;
+    *bytes = plan_workspace(p, d->m, d->n, kNumCUs);
     return ok();
 }
 
@@ -1118,7 +1188,7 @@ int t0g_gemm_kernel_name(const t0g_gemm_desc *d, char *buf, size_t len) {
     t0g_gemm_config cfg;
     GemmPlan p;
     GemmOperands o;
-    int rc = resolve_desc(d, &cfg, &p, &o);
+    int rc = resolve_desc(d, &cfg, &p, &o, true);
     if (rc) return rc;
     snprintf(buf, len, "%s", p.symbol.c_str());
     return ok();
@@ -1178,20 +1248,20 @@ int t0g_gemm_compile(const t0g_gemm_desc *d, t0g_compiled_kernel *out) {
     return ok();
 }
 
-// t0g_gemm with dev->mu held.
-static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d) {
+// t0g_gemm with dev->mu held.  allow_fused = false: split-K with the separate
+// reduce kernel (launches that may overlap another on this device).
+static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d, bool allow_fused = true) {
     t0g_gemm_config cfg;
     GemmPlan p;
     GemmOperands o;
-    int rc = resolve_desc(d, &cfg, &p, &o);
+    int rc = resolve_desc(d, &cfg, &p, &o, allow_fused);
     if (rc) return rc;
     if ((rc = check_usable(dev))) return rc;
     if (d->m == 0 || d->n == 0) return ok();
     uint64_t ws = 0;
-    if (p.stream_k && (rc = ensure_sk_sync(dev))) return rc;
+    if ((p.stream_k || p.fused) && (rc = ensure_sk_sync(dev))) return rc;
     if (p.splits > 1 || p.stream_k) {
-        const size_t need = p.stream_k ? (size_t)sk_grid(p, dev->num_cus) * T0G_SK_SLOT_BYTES
-                                       : (size_t)p.splits * d->m * d->n * 4;
+        const size_t need = plan_workspace(p, d->m, d->n, dev->num_cus);
         if (d->workspace) {
             if (d->workspace_bytes < need)
                 return fail(T0G_ERR_INVALID_ARG, "workspace of %llu bytes, split-K needs %zu",
@@ -1259,8 +1329,9 @@ int t0g_gemm_noalloc(t0g_device *dev, const t0g_gemm_desc *d) {
 }
 
 // Independent GEMMs, round-robin over the device stream and the side streams.
-// Stream-K keeps one control block per device, so grouped GEMMs take the
-// data-parallel schedule instead (stream-K launches must not overlap).
+// Stream-K and the in-kernel split-K reduction keep one control block per
+// device, so grouped GEMMs take the data-parallel schedule and the separate
+// reduce kernel instead (such launches must not overlap).
 int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n) {
     if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
     if (n && !descs) return fail(T0G_ERR_INVALID_ARG, "descs is NULL");
@@ -1321,7 +1392,7 @@ int t0g_gemm_group(t0g_device *dev, const t0g_gemm_desc *descs, uint32_t n) {
         }
         const int s = (int)(i % (uint32_t)(sides + 1)) - 1;   // -1: the device stream
         if (s >= 0) swap_side(s);
-        first_rc = gemm_locked(dev, &d);
+        first_rc = gemm_locked(dev, &d, false);   // concurrent launches: no shared control block
         if (s >= 0) swap_side(s);
     }
     // join whatever was enqueued, also after a failure

@@ -317,6 +317,7 @@ _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 _sig("t0g_set_stream_k_spin_limit", ctypes.c_int, _u32)
 _sig("t0g_debug_stream_k_stall", ctypes.c_int, ctypes.c_int)
+_sig("t0g_set_split_k_mode", ctypes.c_int, _u32)
 
 
 def _check(rc):
@@ -510,6 +511,15 @@ def set_stream_k_spin_limit(polls):
 
 def debug_stream_k_stall(on):
     _check(_lib.t0g_debug_stream_k_stall(1 if on else 0))
+
+
+SPLIT_K_REDUCE_KERNEL, SPLIT_K_IN_KERNEL = 0, 1
+
+
+def set_split_k_mode(mode):
+    """SPLIT_K_REDUCE_KERNEL (default): planes + reduce kernel; SPLIT_K_IN_KERNEL: split-K
+    reduced inside the GEMM kernel where the plan allows it.  Same bits either way."""
+    _check(_lib.t0g_set_split_k_mode(mode))
 
 
 def debug_fail_hip_call(n):

@@ -4,7 +4,7 @@ selection (tile_auto_select, src/t0/tile_ir.rs:471-568).
 
 The metadata reader is checked against the built gfx950 code object, whose
 argument blocks are known from t0g_kernel_args.h (T0gGemmArgs 104 bytes,
-T0gGemmSkArgs 144), and against malformed or foreign input it must refuse
+T0gGemmSkArgs and T0gGemmRedArgs 144), and against malformed or foreign input it must refuse
 without reading out of bounds."""
 import ctypes
 import os
@@ -51,6 +51,8 @@ def _gfx950_elf(blob):
     ("t0g_gemm_64x64_k64_nt_f32_d", 104, None, 256),
     ("t0g_gemm_256x256_k64_nn_bf16_sk", 144, None, 512),
     ("t0g_gemm_256x256_k64_tt_f32_sk", 144, None, 256),
+    ("t0g_gemm_256x256_k64_nn_bf16_r", 144, None, 512),
+    ("t0g_gemm_128x128_k64_nt_f32_r", 144, None, 256),
     ("t0g_splitk_reduce_bf16", 80, 0, 256),
     ("t0g_f32_to_bf16_rne", 32, 0, 256),
 ])
@@ -78,7 +80,7 @@ def test_argument_block_sizes_match_the_header(blob):
                     names.add(part[:-3].decode())
     assert len(names) >= 60
     for s in sorted(names):
-        want = 144 if s.endswith("_sk") else 104
+        want = 144 if s.endswith("_sk") or s.endswith("_r") else 104   # T0gGemmSkArgs / T0gGemmRedArgs
         assert t0g.code_object_kernel_meta(blob, s).kernarg_size == want, s
 
 

@@ -258,14 +258,18 @@ def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
     b = bufs.up(b_nk)
     esz = 4 if out == t0g.F32 else 2
     c = bufs.alloc(m * n * esz, fill=0)
-    d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk)
-    need = t0g.gemm_workspace_size(d)
-    assert need >= sk * m * n * 4
-    ws = bufs.alloc(need, fill=0)
-    d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk, workspace=ws,
-                      workspace_bytes=need)
-    rt.gemm_desc(d)
-    rt.wait_idle()
+    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)   # the planes this test reads stay in the workspace
+    try:
+        d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk)
+        need = t0g.gemm_workspace_size(d)
+        assert need >= sk * m * n * 4
+        ws = bufs.alloc(need, fill=0)
+        d = t0g.gemm_desc(a, b, c, m, n, k, transpose="NT", out_dtype=out, split_k=sk, workspace=ws,
+                          workspace_bytes=need)
+        rt.gemm_desc(d)
+        rt.wait_idle()
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
     planes = rt.read(ws, (sk, m, n), np.float32)
     host = o.splitk_reduce(planes)
     got = rt.read(c, (m, n), np.float32 if out == t0g.F32 else np.uint16)
@@ -296,14 +300,19 @@ def test_split_k_grid_remap_covers_every_slice(rt, bufs, preset, tiles_m, tiles_
     b = bufs.up(b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T))
     c = bufs.alloc(m * n * 4, fill=0)
     cfg = t0g.GemmConfig.preset(preset)
-    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk)
-    need = t0g.gemm_workspace_size(d)
-    ws = bufs.alloc(need, fill=0xFF)
-    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk,
-                      workspace=ws, workspace_bytes=need)
-    assert f"{tile}x{tile}" in t0g.gemm_kernel_name(d)
-    rt.gemm_desc(d)
-    rt.wait_idle()
+    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)   # planes, not tile slots, in the workspace
+    try:
+        d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk)
+        need = t0g.gemm_workspace_size(d)
+        assert need == sk * m * n * 4
+        ws = bufs.alloc(need, fill=0xFF)
+        d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32, config=cfg, split_k=sk,
+                          workspace=ws, workspace_bytes=need)
+        assert f"{tile}x{tile}" in t0g.gemm_kernel_name(d)
+        rt.gemm_desc(d)
+        rt.wait_idle()
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
     planes = rt.read(ws, (sk, m, n), np.float32)
     assert not np.isnan(planes).any(), "a (tile, K slice) pair was not computed"
     kps = k // sk

@@ -155,6 +155,28 @@ def test_gemm_plan_selection_host_only():
         t0g.gemm_kernel_name(t0g.gemm_desc(1, 2, 3, 64, 64, 64, epilogue=t0g.EPI_BIAS_ADD))   # no bias pointer
 
 
+def test_split_k_mode_selects_the_reduction():
+    """By default split-K writes fp32 planes for the reduce kernel; the in-kernel mode
+    takes the _r kernel (which writes the output dtype and sums the planes itself),
+    and only where its plan conditions hold; an unknown mode is refused."""
+    def name(**kw):
+        return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 128, 4096, 4096, transpose="NT",
+                                                  out_dtype=t0g.BF16, **kw))
+    c128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32"
+    t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
+    try:
+        assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_r"
+        assert name(config=c128, split_k=6) == "t0g_gemm_128x128_k64_nt_f32"     # not a power of two
+        assert name(config=c128) == "t0g_gemm_128x128_k64_nt_bf16"                # no split, nothing to sum
+        with pytest.raises(t0g.T0gError) as e:
+            t0g.set_split_k_mode(2)
+        assert e.value.code == t0g.ERR_INVALID_ARG
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32"
+
+
 def test_no_device_on_this_host_is_an_error():
     if t0g.device_count() > 0:
         pytest.skip("a GPU is present")

@@ -297,6 +297,67 @@ def test_gemm_group_workspace_growth_on_the_device_stream():
         r.close()
 
 
+def _hip_runtime():
+    """The HIP runtime libt0g.so is linked against (its streams are what
+    t0g_device_set_stream takes)."""
+    import ctypes
+    hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    return hip
+
+
+def test_stream_switch_orders_split_k_launches():
+    """t0g_device_set_stream: work issued after a switch of stream waits for the work
+    issued on the old one, so two split-K GEMMs that share the handle's workspace run
+    one after the other.  A large split-K GEMM on stream A, a switch to stream B and at
+    once a small one whose planes go to the same workspace: both match the oracle."""
+    import ctypes
+    hip = _hip_runtime()
+    r = t0g.GpuRuntime.new(0)
+    streams = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for s in streams:
+        assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    bufs = []
+    try:
+        def up(arr):
+            a = r.upload(arr)
+            bufs.append(a)
+            return a
+
+        def out(nbytes):
+            a = r.alloc(nbytes)
+            bufs.append(a)
+            return a
+
+        cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+        bm, bn, bk = 1024, 1024, 8192
+        sm, sn, sk_ = 256, 256, 4096
+        x_b, w_b = o.rand_bf16_lcg(bm * bk, 21), o.rand_bf16_lcg(bn * bk, 22)
+        x_s, w_s = o.rand_bf16_lcg(sm * sk_, 23), o.rand_bf16_lcg(sn * sk_, 24)
+        xb, wb, xs, ws = up(x_b), up(w_b), up(x_s), up(w_s)
+        yb, ys = out(bm * bn * 4), out(sm * sn * 4)
+        r.wait_idle()
+        _log("[case] split-K 1024x1024x8192 on stream A, then 256x256x4096 on stream B")
+        r.set_stream(streams[0].value)
+        r.gemm(xb, wb, yb, bm, bn, bk, config=cfg)
+        r.set_stream(streams[1].value)
+        r.gemm(xs, ws, ys, sm, sn, sk_, config=cfg)
+        for s in streams:
+            assert hip.hipStreamSynchronize(s) == 0
+        r.set_stream(None)
+        check_parity(r.read(yb, (bm, bn), np.float32), o.gemm("NT", x_b, w_b, bm, bn, bk), bk, "stream A")
+        check_parity(r.read(ys, (sm, sn), np.float32), o.gemm("NT", x_s, w_s, sm, sn, sk_), sk_, "stream B")
+    finally:
+        r.set_stream(None)
+        for a in bufs:
+            r.free(a)
+        r.close()
+        for s in streams:
+            hip.hipStreamDestroy(s)
+
+
 # ---- buffer pool and f32 helpers ------------------------------------------------
 
 def test_pool_reuses_recycled_buffers(rt):

@@ -1,0 +1,159 @@
+"""Split-K reduced inside the GEMM kernel (the _r kernels), through the C ABI.
+
+The in-kernel reduction sums every chunk of a tile over its K slices in plane
+order from 0.0, the order of the separate reduce kernel and of the reference's
+host loop (examples/test_gemm_correctness.rs:190-207).  So each case runs once
+reduced in the kernel and once as planes plus the reduce kernel
+(t0g_set_split_k_mode) and the two outputs must be identical bit for bit; the
+result is also checked against the oracle.  Cases cover both tiles that have an
+in-kernel form (128x128, 256x256 in its 8-wave and 4-wave kernels), all
+layouts, f32 and bf16 output, ragged M/N edges, K tails, epilogue chains,
+repeated launches (the control words must be back at zero after each) and the
+host-forced path in which every workgroup but a tile's last arrival gives up
+waiting, so the last arrival sums the whole tile."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as o
+import t0g
+
+pytestmark = pytest.mark.gpu
+
+P128 = t0g.GemmConfig.preset("tile_128x128_k64")
+P256 = t0g.GemmConfig.preset("tile_256x256_k64")
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def rt():
+    r = t0g.GpuRuntime.new(0)
+    yield r
+    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+    t0g.debug_stream_k_stall(False)
+    assert r.stream_k_timeouts() == 0
+    r.close()
+
+
+def _operands(layout, m, n, k, seed):
+    a_mk = o.rand_bf16_lcg(m * k, seed).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, seed + 1).reshape(n, k)
+    a_st = a_mk if layout[0] == "N" else np.ascontiguousarray(a_mk.T)
+    b_st = b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T)
+    return a_mk, b_nk, a_st, b_st
+
+
+def _run(rt, da, db, m, n, k, layout, cfg, sk, out, mode, epilogue_ops=None, bias=0, repeat=1):
+    esz, dt = (2, np.uint16) if out == t0g.BF16 else (4, np.float32)
+    t0g.set_split_k_mode(mode)
+    try:
+        d = t0g.gemm_desc(da, db, 0, m, n, k, transpose=layout, out_dtype=out, config=cfg, split_k=sk,
+                          epilogue_ops=epilogue_ops, bias=bias)
+        name = t0g.gemm_kernel_name(d)
+        dc = rt.alloc(m * n * esz)
+        try:
+            rt.memset(dc, 0xFF, m * n * esz)
+            d.c = dc
+            for _ in range(repeat):
+                rt.gemm_desc(d)
+            rt.wait_idle()
+            return name, rt.read(dc, (m, n), dt)
+        finally:
+            rt.free(dc)
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+
+
+CASES = [
+    # layout, m, n, k, config, split: what it exercises
+    ("NT", 128, 4096, 4096, P128, 8),      # benchmark config 4a
+    ("NT", 256, 256, 32768, P128, 64),     # benchmark config 4b: 64 slices per tile, 64-element chunks of 4 rows
+    ("NN", 256, 256, 32768, P256, 64),     # one 256x256 tile in 64 slices (8-wave kernel)
+    ("NN", 1024, 4096, 11008, P256, 4),    # the MLP's Y = H W2: 64 tiles x 4 slices, K tail per slice
+    ("NT", 1024, 4096, 11008, P256, 4),    # the MLP's dX = dH W1^T
+    ("TN", 512, 768, 4096, P256, 8),       # 4-wave 256x256 kernel (M-contiguous A)
+    ("TT", 384, 512, 2048, P256, 4),       # ragged M on the 4-wave kernel
+    ("TN", 200, 296, 4096, P128, 4),       # ragged M and N on 128x128
+    ("NN", 320, 136, 3000, P128, 4),       # K tail: 3000 in slices of 768
+    ("TT", 128, 128, 8192, P128, 32),      # a single tile in 32 slices
+]
+
+
+@pytest.mark.parametrize("out", [t0g.F32, t0g.BF16])
+@pytest.mark.parametrize("layout,m,n,k,cfg,sk", CASES)
+def test_fused_equals_reduce_kernel(rt, layout, m, n, k, cfg, sk, out):
+    _log(f"[case] fused split-K {layout} {m}x{n}x{k} {cfg.tile_m}x{cfg.tile_n} sk={sk} out={out}")
+    a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 101 + m + sk)
+    da, db = rt.upload(a_st), rt.upload(b_st)
+    try:
+        name_f, fused = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_IN_KERNEL)
+        name_r, planes = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_REDUCE_KERNEL)
+        assert name_f.endswith("_r") and not name_r.endswith("_r"), (name_f, name_r)
+        assert np.array_equal(fused, planes), f"{name_f} differs from planes + reduce kernel"
+        got = fused if out == t0g.F32 else o.bf16_to_f32(fused)
+        ok, relf, maxabs, bound = o.parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k)
+        _log(f"[parity] {name_f}: identical to the reduce kernel; relF={relf:.3e} max|d|={maxabs:.3e}")
+        assert ok if out == t0g.F32 else relf <= 5e-3
+    finally:
+        rt.free(da)
+        rt.free(db)
+
+
+@pytest.mark.parametrize("layout,m,n,k,cfg,sk", [CASES[0], CASES[3], CASES[7]])
+def test_fused_epilogue_chain(rt, layout, m, n, k, cfg, sk):
+    """bias + SiLU + clamp applied once, after the sum (not per slice)."""
+    a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 7 + n)
+    bias = np.linspace(-0.5, 0.5, n, dtype=np.float32)
+    da, db, dbias = rt.upload(a_st), rt.upload(b_st), rt.upload(bias)
+    ops = ["bias", "silu", "clamp"]
+    try:
+        t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
+        d = t0g.gemm_desc(da, db, 0, m, n, k, transpose=layout, config=cfg, split_k=sk, epilogue_ops=ops,
+                          bias=dbias, clamp=(-0.05, 0.1))
+        dc = rt.alloc(m * n * 4)
+        try:
+            d.c = dc
+            rt.gemm_desc(d)
+            fused = rt.read(dc, (m, n), np.float32)
+            t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+            rt.gemm_desc(d)
+            planes = rt.read(dc, (m, n), np.float32)
+        finally:
+            t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+            rt.free(dc)
+        assert np.array_equal(fused, planes)
+        ref = o.epilogue_chain(o.gemm("NT", a_mk, b_nk, m, n, k), ops, bias=bias, clamp=(-0.05, 0.1))
+        ok, relf, maxabs, _ = o.parity(fused, ref, k)
+        assert ok, (relf, maxabs)
+    finally:
+        for x in (da, db, dbias):
+            rt.free(x)
+
+
+def test_fused_repeated_launches_and_stall(rt):
+    """Eight launches back to back give the same bits (the arrival and claim words
+    are reset by every launch); with the host-forced stall every tile is summed by
+    its last arrival alone, with the same bits; no launch counts a timeout."""
+    layout, m, n, k, cfg, sk = CASES[0]
+    a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 55)
+    da, db = rt.upload(a_st), rt.upload(b_st)
+    try:
+        _, once = _run(rt, da, db, m, n, k, layout, cfg, sk, t0g.F32, t0g.SPLIT_K_IN_KERNEL)
+        _, eight = _run(rt, da, db, m, n, k, layout, cfg, sk, t0g.F32, t0g.SPLIT_K_IN_KERNEL, repeat=8)
+        assert np.array_equal(once, eight)
+        t0g.debug_stream_k_stall(True)
+        try:
+            _, alone = _run(rt, da, db, m, n, k, layout, cfg, sk, t0g.F32, t0g.SPLIT_K_IN_KERNEL, repeat=3)
+        finally:
+            t0g.debug_stream_k_stall(False)
+        assert np.array_equal(once, alone)
+        assert rt.stream_k_timeouts() == 0
+        assert not rt.is_poisoned()
+    finally:
+        rt.free(da)
+        rt.free(db)
