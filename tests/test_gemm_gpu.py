@@ -85,7 +85,14 @@ def run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, out=t0g.F32, **kw):
 
 def check_parity(c_gpu, c_ref, k, label):
     ok, relf, maxabs, bound = o.parity(c_gpu, c_ref, k)
-    _log(f"[parity] {label}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
+    line = f"[parity] {label}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})"
+    _log(line)
+    # T0G_PARITY_LOG=<file>: every comparison is also appended there, so a run whose
+    # passing tests' output pytest swallows still leaves the per-config figures
+    log_path = os.environ.get("T0G_PARITY_LOG")
+    if log_path:
+        with open(log_path, "a") as f:
+            f.write(line + ("" if ok else "  FAIL") + "\n")
     assert ok, f"{label}: relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
 
 
