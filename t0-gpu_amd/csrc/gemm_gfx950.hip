@@ -924,13 +924,21 @@ __device__ __forceinline__ void mfma_rows(f32x16_t (&acc)[SM][SN], const bf16x8_
 }
 
 // The K loop of the fast path (128x128 and 64x64 tiles): ring of NS >= 4
-// stages of BK 32, DMA NS-1 stages ahead, one barrier per stage.
+// stages of BK 32 or 64, DMA NS-1 stages ahead, one barrier per stage.  A
+// stage's BK / 16 K steps alternate between two fragment register sets; the
+// stage's DMA instructions are spread evenly over its steps.  BK 64 makes each
+// K-contiguous LDS row a whole 128-byte line, so every DMA request fetches
+// complete cache lines (the deep-ring kernels, one workgroup per CU).
 template <bool CHECK, uint32_t BK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN,
           class OpA, class OpB>
 __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& la, const OpB& lb, const T0gGemmArgs& p,
                                            uint32_t a_bytes, uint32_t b_bytes, uint32_t kbeg, uint32_t kend, int nst,
                                            uint32_t lds0) {
-    static_assert(BK == 32 && NS >= 4, "ring of BK 32 stages");
+    static_assert((BK == 32 || BK == 64) && NS >= 4, "ring of BK 32 or 64 stages");
+    constexpr int kSteps = (int)BK / 16;
+    // DMA instructions of the stage before K step i: [kD(i), kD(i + 1))
+    constexpr int kPer = (kVmemPerStage + kSteps - 1) / kSteps;
+#define T0G_KD(i) ((i) * kPer < kVmemPerStage ? (i) * kPer : kVmemPerStage)
     bf16x8_t fa0[SM], fb0[SN], fa1[SM], fb1[SN];
     {
         // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
@@ -944,7 +952,6 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
         la.template read<0>(lds0, fa0);
         lb.template read<0>(lds0 + A_BYTES, fb0);
 
-        constexpr int kHalf = (kVmemPerStage + 1) / 2;
         uint32_t cur = 0;                 // byte offset of stage s's buffer
         uint32_t fill = (NS - 1) * STAGE; // buffer receiving stage s + NS - 1
         for (int s = 0; s < nst; ++s) {
@@ -952,18 +959,25 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
             const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * BK;
             const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
             const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
-            // K step 0 of stage s (reads: step 1 of stage s), then K step 1
-            // (reads: step 0 of stage s+1, landed before the last barrier).
-            mfma_rows<0, 2, 0, kHalf, CHECK>(acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill,
-                                      ra, rb, kf, kend);
-            mfma_rows<1, 2, kHalf, kVmemPerStage - kHalf, CHECK>(acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur,
-                                                           lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+            // K step i of stage s reads step i + 1's fragments (the last step:
+            // step 0 of stage s + 1, landed before the last barrier).
+            mfma_rows<0, kSteps, T0G_KD(0), T0G_KD(1) - T0G_KD(0), CHECK>(
+                acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+            mfma_rows<1, kSteps, T0G_KD(1), T0G_KD(2) - T0G_KD(1), CHECK>(
+                acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+            if constexpr (kSteps == 4) {
+                mfma_rows<2, kSteps, T0G_KD(2), T0G_KD(3) - T0G_KD(2), CHECK>(
+                    acc, fa0, fb0, fa1, fb1, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+                mfma_rows<3, kSteps, T0G_KD(3), T0G_KD(4) - T0G_KD(3), CHECK>(
+                    acc, fa1, fb1, fa0, fb0, la, lb, lds0 + cur, lds0 + nxt, lds0 + fill, ra, rb, kf, kend);
+            }
             T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // stage s+2 has landed
             barrier_no_fence();
             fill = cur;
             cur = nxt;
         }
     }
+#undef T0G_KD
 }
 
 }  // namespace t0g
@@ -983,7 +997,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int SM = WTM / 32, SN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-    static_assert(BK == 32 && NS >= 4, "unsupported pipeline shape");
+    static_assert((BK == 32 || BK == 64) && NS >= 4, "unsupported pipeline shape");
     using OpA = DmaOperand<A_K, BM, NT, SM, BK>;
     using OpB = DmaOperand<B_K, BN, NT, SN, BK>;
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
@@ -1245,11 +1259,16 @@ extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvert
     T0G_GEMM_LAYOUTS(PFX, BM, BN, WM, WN, f32, false, _u, false) \
     T0G_GEMM_LAYOUTS(PFX, BM, BN, WM, WN, bf16, true, _u, false)
 
-// Deep-ring variant (suffix _d) of the 64x64 tile for grids of at most one
-// workgroup per CU (split-K shapes): 128 KB of LDS per workgroup keeps 15
-// stages of DMA in flight instead of 3, covering HBM latency with a single
-// workgroup on the CU.
-#define T0G_PIPE_D_64x64 32, 16
+// Deep-ring variants (suffix _d) of the 64x64 and 128x128 tiles for grids of
+// at most one workgroup per CU (split-K and thin shapes): 128 KB of LDS per
+// workgroup in stages of 64 K values, so every K-contiguous LDS row is a whole
+// 128-byte line and each DMA request fetches full cache lines (half-line
+// requests of the 32-K stages left a single workgroup per CU well short of
+// the CU's fill rate: 256x256x32768 split 16 went from 17.7 to 15.0 us,
+// 1024x4096x11008 on 128x128 tiles from 116 to 83 us).  64x64: 8 stages, 7 in
+// flight; 128x128: 4 stages, 3 in flight.
+#define T0G_PIPE_D_64x64 64, 8
+#define T0G_PIPE_D_128x128 64, 4
 #define T0G_GEMM_D(NAME, BM, BN, WM, WN, AK, BKM, OBF)                                                           \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))       \
         NAME(T0gGemmArgs p) {                                                                                  \
@@ -1350,6 +1369,7 @@ T0G_GEMM_TILE(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_TILE_U(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_D(t0g_gemm_64x64_k64, 64, 64, 2, 2)
+T0G_GEMM_TILE_D(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 
 extern "C" __global__ void __launch_bounds__(256) t0g_splitk_reduce_f32(T0gReduceArgs p) {
     t0g::splitk_reduce<false>(p);

@@ -37,12 +37,14 @@ int ok() {
 // the power-limited shader clock that data draws): time per wave of
 // workgroups = t0_us + (per-CU FLOP) / rate, linear in K to within a few
 // percent over K = 256 .. 8192.  64x64 gains throughput from co-resident
-// workgroups, 128x128 does not (one already saturates the CU's LDS traffic).
-// 256x256 runs 8 waves (two per SIMD, in ping-pong).
+// workgroups.  256x256 runs 8 waves (two per SIMD, in ping-pong).  Grids of at
+// most one workgroup per CU run the 64x64 and 128x128 deep-ring kernels, whose
+// fixed cost and rate were fitted on 256-workgroup grids over K = 512 .. 8192
+// (1024^2 and 2048^2 outputs); 128x128's two-workgroup rate on 4096^2 outputs.
 const TileDef kTiles[kNumTiles] = {
-    {256, 256, 512, 1, 13.9, 5243.0, 5243.0, "t0g_gemm_256x256_k64"},
-    {128, 128, 256, 2, 6.7, 3034.0, 3034.0, "t0g_gemm_128x128_k64"},
-    {64, 64, 256, 4, 2.6, 931.0, 1606.0, "t0g_gemm_64x64_k64"},
+    {256, 256, 512, 1, 13.9, 5243.0, 5243.0, 0.0, 0.0, "t0g_gemm_256x256_k64"},
+    {128, 128, 256, 2, 4.75, 3628.0, 3628.0, 4.83, 4590.0, "t0g_gemm_128x128_k64"},
+    {64, 64, 256, 4, 2.6, 931.0, 1606.0, 3.54, 2186.0, "t0g_gemm_64x64_k64"},
 };
 
 const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size) {
@@ -109,11 +111,13 @@ double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint3
     const double per_cu = ceil(wgs / kNumCUs);
     const double resident = per_cu < t.wg_per_cu ? per_cu : (double)t.wg_per_cu;
     const double waves = ceil(per_cu / t.wg_per_cu);
-    const double rate = t.wg_per_cu > 1
+    const bool deep = tile_uses_deep(t, (uint64_t)wgs);
+    const double rate = deep ? t.rate_deep
+                        : t.wg_per_cu > 1
                             ? t.rate1 + (t.rate_full - t.rate1) * (resident - 1.0) / (double)(t.wg_per_cu - 1)
                             : t.rate1;
     const double flops_cu = per_cu * 2.0 * t.bm * t.bn * (kc > 0 ? kc : (double)kTileK);
-    double t_us = waves * t.t0_us + flops_cu / rate * 1e-3;
+    double t_us = (deep ? t.t0_deep_us : waves * t.t0_us) + flops_cu / rate * 1e-3;
     const double bytes = 2.0 * ((double)m * k + (double)k * n) + 2.0 * (double)m * n;
     const double t_mem = bytes / kPeakBytes * 1e6;
     if (t_mem > t_us) t_us = t_mem;

@@ -26,10 +26,18 @@ struct TileDef {
     double t0_us;           // per-wave fixed cost: prologue, epilogue, launch share
     double rate1;           // per-CU bf16 FLOP/ns with one resident workgroup
     double rate_full;       // per-CU bf16 FLOP/ns with wg_per_cu resident workgroups
+    double t0_deep_us;      // the deep-ring kernel (grids of at most one workgroup per CU):
+    double rate_deep;       //   fixed cost and per-CU rate; 0 for tiles without one
     const char *symbol_prefix;
 };
 constexpr int kNumTiles = 3;
 extern const TileDef kTiles[kNumTiles];
+// The 64x64 and 128x128 tiles run their deep-ring kernels (suffix _d: one
+// workgroup per CU, 64-K stages) when the grid gives each CU at most one
+// workgroup.
+inline bool tile_uses_deep(const TileDef &t, uint64_t workgroups) {
+    return (t.bm == 64 || t.bm == 128) && workgroups <= kNumCUs;
+}
 
 extern thread_local std::string g_last_error;
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -311,11 +311,10 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
                (tile->bm == 256 || tile->bm == 128) && (sk & (sk - 1)) == 0 && sk <= kMaxSplitK &&
                red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
                red_grid * tile->bm * tile->bn * 4 < (1ull << 31);
-    // At most one workgroup per CU: the 64x64 tile switches to its deep-ring
-    // variant (the CU's LDS then holds one workgroup with 128 KB of stages;
-    // measured 10 % faster on 256x256x32768 split 16, while 128x128 gained
-    // nothing on 128x4096x4096 split 8 and keeps its 4-stage ring).
-    const bool deep = aligned && !wide && tile->bm == 64 && (uint64_t)p->tiles_m * p->tiles_n * sk <= kNumCUs;
+    // At most one workgroup per CU: the 64x64 and 128x128 tiles switch to their
+    // deep-ring variants (the CU's LDS then holds one workgroup with 128 KB of
+    // 64-K stages, whole cache lines per DMA request).
+    const bool deep = tile_uses_deep(*tile, (uint64_t)p->tiles_m * p->tiles_n * sk) && aligned && !wide && !p->fused;
     // The 256x256 kernels with a K-contiguous A (NN, NT) run 8 waves in
     // ping-pong; with an M-contiguous A (TN, TT) every fragment is a transposed
     // LDS read and the 4-wave kernel, with half the fragment reads per CU, is

@@ -163,18 +163,22 @@ def test_split_k_mode_selects_the_reduction():
         return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 128, 4096, 4096, transpose="NT",
                                                   out_dtype=t0g.BF16, **kw))
     c128 = t0g.GemmConfig.preset("tile_128x128_k64")
-    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32"
+    # 32 tiles x 8 slices: one workgroup per CU, so the deep-ring kernel writes the planes
+    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
     t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
     try:
         assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_r"
-        assert name(config=c128, split_k=6) == "t0g_gemm_128x128_k64_nt_f32"     # not a power of two
-        assert name(config=c128) == "t0g_gemm_128x128_k64_nt_bf16"                # no split, nothing to sum
+        assert name(config=c128, split_k=6) == "t0g_gemm_128x128_k64_nt_f32_d"   # not a power of two
+        assert name(config=c128) == "t0g_gemm_128x128_k64_nt_bf16_d"              # no split, nothing to sum
         with pytest.raises(t0g.T0gError) as e:
             t0g.set_split_k_mode(2)
         assert e.value.code == t0g.ERR_INVALID_ARG
     finally:
         t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
-    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32"
+    assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
+    # more workgroups than CUs: the 4-stage ring kernel, two workgroups per CU
+    assert t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, out_dtype=t0g.BF16,
+                                              config=c128)) == "t0g_gemm_128x128_k64_nt_bf16"
 
 
 def test_no_device_on_this_host_is_an_error():
