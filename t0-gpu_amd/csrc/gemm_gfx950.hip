@@ -309,22 +309,31 @@ __device__ __forceinline__ void apply_epilogue_n(float (&v)[N], const float (&bv
 // Output tile index and K slice of this workgroup (grid x is exactly the tile
 // count, grid y the split count).  The dispatcher deals workgroups out to the
 // 8 XCDs round-robin in linear order (x fastest).  With XCD_REMAP the linear id
-// is permuted so that XCD c owns the contiguous range [c*total/8, (c+1)*total/8)
-// of slice-major (split, tile) order: the workgroups of one K slice share an
-// L2, which then fetches each A and B panel of that slice once instead of once
-// per XCD.  Without split-K this is the plain tile remap.  (The 256x256
-// kernels keep the tile-only remap: measured, the extra prologue work cost
-// their 4096^3 launch 1-1.5 %, more than the split-K shapes on that tile gain.)
+// is permuted so that XCD c owns a contiguous range of slice-major (split,
+// tile) order (xcd_range): the workgroups of one K slice share an L2, which
+// then fetches each A and B panel of that slice once instead of once per XCD.
+// Without split-K this is the plain tile remap.  (The 256x256 kernels keep the
+// tile-only remap: measured, the extra prologue work cost their 4096^3 launch
+// 1-1.5 %, more than the split-K shapes on that tile gain.)
 struct GridPos {
     uint32_t tile, split;
 };
+
+// Linear workgroup id -> position in an order where XCD c (ids = c mod 8)
+// holds one contiguous range: of `total` items, XCDs below total % 8 get
+// total / 8 + 1 consecutive items and the others total / 8, so every id maps
+// to a distinct item whatever the count (a bijection of [0, total)).
+__device__ __forceinline__ uint32_t xcd_range(uint32_t id, uint32_t total) {
+    const uint32_t x = id & 7u, q = total >> 3, r = total & 7u;
+    return x * q + min(x, r) + (id >> 3);
+}
+
 __device__ __forceinline__ GridPos grid_pos(const T0gGemmArgs& p) {
     const uint32_t nblk = p.tiles_m * p.tiles_n;
     uint32_t tile = blockIdx.x, split = blockIdx.y;
     const uint64_t total = (uint64_t)nblk * gridDim.y;
-    if ((p.flags & T0G_FLAG_XCD_REMAP) && (total & 7u) == 0 && total <= 0xFFFFFFFFull) {
-        const uint32_t lin = split * nblk + tile;
-        const uint32_t l = (lin & 7u) * (uint32_t)(total >> 3) + (lin >> 3);
+    if ((p.flags & T0G_FLAG_XCD_REMAP) && total <= 0xFFFFFFFFull) {
+        const uint32_t l = xcd_range(split * nblk + tile, (uint32_t)total);
         split = l / nblk;
         tile = l - split * nblk;
     }

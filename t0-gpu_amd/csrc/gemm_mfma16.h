@@ -358,11 +358,120 @@ struct SkFixup {
     uint32_t frag;
 };
 
+// bf16 epilogue of a wave's SM x SN sub-tiles of a tile wholly inside an aligned
+// C, converted in registers and staged as bf16.  The chain and the RNE
+// conversion run on the MFMA result layout (lane (q, c) of sub-tile (i, j)
+// holds rows 4q .. 4q+3 of column 16 j + c, one bias value per lane and j).
+// Each 16-row band of the wave's tile then goes through LDS column-major, 32
+// bytes (16 rows, four 8-byte pieces) per column: one ds_write_b64 per lane and
+// sub-tile puts the lane's 4 rows in place.  ds_read_b64_tr_b16 hands lane i of
+// a 16-lane group element i % 4 of the pieces that lanes 4 r + i / 4 (r =
+// 0..3) of the group address; with lane 4 r + s of group g addressing column
+// 16 g + 8 (s & 1) + r (+ 4 in the second read) and piece 2 p + (s >> 1), lane
+// i = 4 s + e receives row 8 p + 4 (s >> 1) + e, columns 16 g + 8 (s & 1) ..
+// + 7 (16 bytes), and one store instruction writes 8 rows x 64 columns: whole
+// 128-byte lines.  Column col is placed at col ^ 4 in odd 8-column blocks and
+// its pieces XORed with 2 when bit 3 and bit 4 of col differ, which puts the
+// 32 lanes of every half-wave access -- writes: 16 columns x 2 pieces; reads:
+// two groups of 8 columns x 2 pieces -- on distinct banks.  Against staging
+// fp32 rows this halves the LDS bytes and takes a quarter of the LDS write
+// instructions.  Two bands alternate between two regions, so a band's writes
+// never wait for the previous band's reads.  `lds`: 2 * SN * 512 bytes of this
+// wave's own.
+__device__ __forceinline__ uint32_t bf16_stage_off(uint32_t col, uint32_t piece) {
+    const uint32_t b3 = (col >> 3) & 1u, b4 = (col >> 4) & 1u;
+    return (col ^ (b3 << 2)) * 32u + (piece ^ ((b3 ^ b4) << 1)) * 8u;
+}
+
+// One accumulator read out of its AGPR at this point of the program.  The
+// register allocator otherwise copies every accumulator a VALU instruction
+// uses into VGPRs right after the K loop -- all 128 (or 256) of them at once,
+// more than the VGPRs left -- and spills.
+__device__ __forceinline__ float acc_read(float a) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+
+template <int SM, int SN>
+__device__ __forceinline__ void store_tile_bf16_tr(const T0gGemmArgs& p, const f32x4_t (&acc)[SM][SN], uint32_t row0,
+                                                   uint32_t col0, uint32_t lane, uint32_t lds) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) u32x2_t lds_u32x2;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    static_assert(SN % 4 == 0, "the wave tile's columns come in blocks of 64");
+    constexpr uint32_t kRegion = SN * 16 * 32;   // one band: 16 rows x 16 SN columns of bf16
+    // The lane index through an opaque move: every address and bias value below
+    // derives from it, so none of them is hoisted above the K loop's (volatile)
+    // MFMAs and held in registers across it.
+    asm volatile("v_mov_b32 %0, %0" : "+v"(lane));
+    const uint32_t l16 = lane & 15u, q = lane >> 4;
+    const EpiParams ep = epi_of(p);
+    float bv[SN];
+#pragma unroll
+    for (int j = 0; j < SN; ++j)
+        bv[j] = (p.flags & T0G_FLAG_BIAS)
+                    ? reinterpret_cast<const __attribute__((address_space(1))) float*>(p.bias)[col0 + j * 16 + l16]
+                    : 0.0f;
+    // read side: lane 16 g + 4 r + s
+    const uint32_t g = lane >> 4, r = (lane >> 2) & 3u, s = lane & 3u, e = lane & 3u;
+    const uint32_t rcol = 16u * g + 8u * (s & 1u) + r, rpc = s >> 1;
+    // the lane's own row and columns in the band after the two reads of pair pp
+    const uint32_t srow = 4u * ((l16 >> 2) >> 1) + e, scol = 16u * g + 8u * ((l16 >> 2) & 1u);
+    const uint64_t cb = p.c + ((uint64_t)(row0 + srow) * p.ldc + col0 + scol) * 2u;
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        // one band at a time
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t reg = lds + (uint32_t)(i & 1) * kRegion;
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            float v[4] = {acc_read(acc[i][j][0]), acc_read(acc[i][j][1]), acc_read(acc[i][j][2]),
+                          acc_read(acc[i][j][3])};
+            const float b4[4] = {bv[j], bv[j], bv[j], bv[j]};
+            apply_epilogue_n<4>(v, b4, ep);
+            u32x2_t w;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                w[h] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * h]) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * h + 1]) << 16);
+            *reinterpret_cast<lds_u32x2*>((uintptr_t)(reg + bf16_stage_off(16u * j + l16, q))) = w;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < SN / 4; ++u)
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                const uint32_t c0 = 64u * u + rcol, piece = 2u * pp + rpc;
+                const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_v4s*)(uintptr_t)(reg + bf16_stage_off(c0, piece)));
+                const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_v4s*)(uintptr_t)(reg + bf16_stage_off(c0 + 4u, piece)));
+                u32x4_t w;
+                w[0] = __builtin_bit_cast(uint32_t, __builtin_shufflevector(lo, lo, 0, 1));
+                w[1] = __builtin_bit_cast(uint32_t, __builtin_shufflevector(lo, lo, 2, 3));
+                w[2] = __builtin_bit_cast(uint32_t, __builtin_shufflevector(hi, hi, 0, 1));
+                w[3] = __builtin_bit_cast(uint32_t, __builtin_shufflevector(hi, hi, 2, 3));
+                const uint64_t addr = cb + ((uint64_t)(16u * i + 8u * pp) * p.ldc + 64u * u) * 2u;
+                __builtin_nontemporal_store(
+                    w, reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)addr));
+            }
+    }
+}
+
 // WT: 16-byte stores write through to memory (sc0 sc1), as in store_tile_vec.
 template <int SM, int SN, bool OUT_BF16, bool FIXUP = false, bool WT = false>
 __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32x4_t (&acc)[SM][SN], uint32_t row0,
                                                  uint32_t col0, uint32_t lane, uint32_t lds, bool vec,
                                                  SkFixup fx = SkFixup{0, 0, 0, 0}) {
+    if constexpr (OUT_BF16 && !FIXUP && !WT) {
+        static_assert(2 * SN * 512 <= VecEpilogue16<SN>::kWaveBytes, "bf16 staging fits the wave's region");
+        if (vec) {
+            store_tile_bf16_tr<SM, SN>(p, acc, row0, col0, lane, lds);
+            return;
+        }
+    }
     typedef VecEpilogue16<SN> E;
     typedef __attribute__((address_space(3))) float lds_f32;
     typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
@@ -488,7 +597,7 @@ template <int BM, int BN>
 __device__ __forceinline__ void tile_origin(const T0gGemmArgs& p, uint32_t& m0, uint32_t& n0) {
     uint32_t bid = blockIdx.x;
     const uint32_t nblk = p.tiles_m * p.tiles_n;
-    if ((p.flags & T0G_FLAG_XCD_REMAP) && (nblk & 7u) == 0) bid = (bid & 7u) * (nblk >> 3) + (bid >> 3);
+    if (p.flags & T0G_FLAG_XCD_REMAP) bid = xcd_range(bid, nblk);
     const uint32_t gm = p.group_m;
     const uint32_t per_group = gm * p.tiles_n;
     const uint32_t group = bid / per_group;

@@ -290,11 +290,13 @@ def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
 @pytest.mark.parametrize("preset", ["tile_64x64_k64", "tile_128x128_k64"])
 @pytest.mark.parametrize("tiles_m,tiles_n,sk,layout", [(1, 1, 8, "NT"), (2, 2, 2, "NN"), (1, 3, 8, "TN"),
                                                        (2, 3, 4, "NT"), (4, 4, 16, "NN"), (1, 5, 8, "NT"),
-                                                       (3, 2, 4, "TT"), (2, 4, 3, "NT")])
+                                                       (3, 2, 4, "TT"), (2, 4, 3, "NT"), (1, 7, 3, "NN"),
+                                                       (3, 5, 2, "TN"), (5, 3, 3, "NT"), (1, 1, 2, "TT")])
 def test_split_k_grid_remap_covers_every_slice(rt, bufs, preset, tiles_m, tiles_n, sk, layout):
-    """Split-K grids of 8k workgroups on the 128x128 and 64x64 tiles are permuted
-    slice-major over the XCDs; every (tile, K slice) pair must still be computed
-    exactly once.  The partial planes start as NaN (0xFF bytes), so a pair the
+    """Split-K grids on the 128x128 and 64x64 tiles are permuted slice-major over
+    the XCDs, each XCD a contiguous range whatever the workgroup count (21, 30, 45
+    and 2 here are not multiples of 8); every (tile, K slice) pair must still be
+    computed exactly once.  The partial planes start as NaN (0xFF bytes), so a pair the
     permutation skipped would leave NaN in its plane; each plane is checked
     against the oracle's product over that slice, and the reduced output
     against the whole product (ragged N edge included)."""
@@ -330,6 +332,31 @@ def test_split_k_grid_remap_covers_every_slice(rt, bufs, preset, tiles_m, tiles_
     got = rt.read(c, (m, n), np.float32)
     assert np.array_equal(got.view(np.uint32), o.splitk_reduce(planes).view(np.uint32))
     check_parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"split remap {tiles_m}x{tiles_n} sk={sk}")
+
+
+@pytest.mark.parametrize("tiles_m,tiles_n,layout", [(3, 5, "NN"), (1, 7, "NT"), (4, 43, "NN"), (5, 3, "TN"),
+                                                    (2, 9, "TT")])
+def test_tile_remap_256_covers_every_tile(rt, bufs, tiles_m, tiles_n, layout):
+    """The 256x256 kernels remap block ids so each XCD owns a contiguous range of
+    tiles, also when the tile count is not a multiple of 8 (15, 7, 172 -- the MLP
+    forward -- 15 and 18 here).  C starts as NaN (0xFF bytes), so a tile the
+    permutation skipped stays NaN; the whole output is checked against the oracle
+    (ragged M and N edges included)."""
+    m, n, k = tiles_m * 256 - 24, tiles_n * 256 - 40, 192
+    _log(f"[case] 256 remap {tiles_m}x{tiles_n} tiles {layout}")
+    a_mk = o.rand_bf16_lcg(m * k, 23 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 29 + n).reshape(n, k)
+    a = bufs.up(a_mk if layout[0] == "N" else np.ascontiguousarray(a_mk.T))
+    b = bufs.up(b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T))
+    c = bufs.alloc(m * n * 4, fill=0xFF)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32,
+                      config=t0g.GemmConfig.preset("tile_256x256_k64"))
+    assert "256x256" in t0g.gemm_kernel_name(d)
+    rt.gemm_desc(d)
+    rt.wait_idle()
+    got = rt.read(c, (m, n), np.float32)
+    assert not np.isnan(got).any(), "an output tile was not computed"
+    check_parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"256 remap {tiles_m}x{tiles_n} {layout}")
 
 
 def _randn_pair(m, n, k, seed_a=2, seed_b=3):
