@@ -412,6 +412,46 @@ def cpu_baseline(torch, tensors, m, n, k, min_seconds):
                                     "sample": f"{rows} output rows of {m}x{n}x{k}, reference loop order"}}
 
 
+def timeline_summary(t0g, torch, rt, desc, k):
+    """One launch's per-workgroup timeline (t0g_set_timeline), recorded as the last
+    of 20 back-to-back launches (steady clock, a queue of work ahead of it), in
+    microseconds from the first workgroup's entry: the launch's span, and per XCD
+    the mean K-loop time (entry to the end of the K loop, first DMA wait
+    included), the mean epilogue time (stores completed) and the last
+    workgroup's end."""
+    import numpy as np
+    rt.timeline_clear()
+    t0g.set_timeline(True)
+    try:
+        for _ in range(20):
+            rt.gemm_desc(desc)
+        torch.cuda.synchronize()
+        tl = rt.timeline_read()
+    finally:
+        t0g.set_timeline(False)
+    rows = tl[tl[:, 0] != 0].astype(np.float64)
+    if len(rows) == 0:
+        return {"workgroups": 0, "note": "the kernel records no timeline"}
+    us = t0g.TIMELINE_TICK_NS / 1e3
+    t0 = rows[:, 0].min()
+    entry, kend, end = (rows[:, 0] - t0) * us, (rows[:, 1] - t0) * us, (rows[:, 2] - t0) * us
+    xcc = (tl[tl[:, 0] != 0][:, 3] >> np.uint64(32)).astype(np.int64) & 15
+    kl, ep = kend - entry, end - kend
+    per_xcd = {}
+    for x in sorted(set(xcc.tolist())):
+        sel = xcc == x
+        per_xcd[str(x)] = {"workgroups": int(sel.sum()), "kloop_us_mean": round(float(kl[sel].mean()), 2),
+                           "epilogue_us_mean": round(float(ep[sel].mean()), 2),
+                           "last_end_us": round(float(end[sel].max()), 2)}
+    return {"workgroups": int(len(rows)), "span_us": round(float(end.max()), 2),
+            "kloop_us": {"min": round(float(kl.min()), 2), "median": round(float(np.median(kl)), 2),
+                         "max": round(float(kl.max()), 2)},
+            "epilogue_us": {"min": round(float(ep.min()), 2), "median": round(float(np.median(ep)), 2),
+                            "max": round(float(ep.max()), 2)},
+            "last_entry_us": round(float(entry.max()), 2), "per_xcd": per_xcd,
+            "clock": "s_memrealtime, 100 MHz"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,6 +462,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other benchmark configurations")
     ap.add_argument("--no-clock", action="store_true", help="skip the shader-clock sampling (amd-smi) lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="with --only LAYOUT:M:N:K: also record one launch's per-workgroup timeline (entry, end "
+                         "of the K loop, stores done; t0g_set_timeline) and print its per-XCD summary")
     ap.add_argument("--only", metavar="LAYOUT:M:N:K",
                     help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
                          "COPY:MiB instead times a plain device-to-device copy of that size, the "
@@ -490,10 +533,13 @@ def main():
         m, n, k = int(m), int(n), int(k)
         r = time_gemm(t0g, torch, rt, stream, m, n, k, lay.upper(), args.steps, args.warmup)
         sec = r["event_ms_per_launch"] * 1e-3
-        print(json.dumps({"only": args.only, "kernel": r["kernel"], "us_per_launch": round(sec * 1e6, 2),
-                          "tflops": round(r["flop"] / sec / 1e12, 2),
-                          "frac_of_peak": round(r["flop"] / sec / 1e12 / PEAK_TFLOPS, 4),
-                          "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1)}), flush=True)
+        line = {"only": args.only, "kernel": r["kernel"], "us_per_launch": round(sec * 1e6, 2),
+                "tflops": round(r["flop"] / sec / 1e12, 2),
+                "frac_of_peak": round(r["flop"] / sec / 1e12 / PEAK_TFLOPS, 4),
+                "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1)}
+        if args.timeline:
+            line["timeline"] = timeline_summary(t0g, torch, rt, r["desc"], k)
+        print(json.dumps(line), flush=True)
         rt.set_stream(None)
         rt.close()
         return

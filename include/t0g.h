@@ -537,6 +537,24 @@ T0G_API int t0g_debug_stream_k_stall(int on);
 #define T0G_SPLIT_K_REDUCE_KERNEL 0u
 #define T0G_SPLIT_K_IN_KERNEL 1u
 T0G_API int t0g_set_split_k_mode(uint32_t mode);
+/* Workgroup timeline, a diagnostic with no reference counterpart (the
+ * reference times whole dispatches on the host clock).  on != 0: later
+ * t0g_gemm launches run the same kernels from a second, instrumented code
+ * object, whose 256x256, 128x128 and 64x64 fast kernels record, per
+ * linear workgroup id (blockIdx.y * gridDim.x + blockIdx.x, the first
+ * T0G_TIMELINE_SLOTS = 8192 of them), four u64 in a per-device array: the GPU's
+ * constant 100 MHz clock at workgroup entry, after the K loop and after the
+ * epilogue's stores completed, then XCC_ID << 32 | HW_ID (the XCD and the
+ * CU/SIMD/wave of the recording wave).  Later launches overwrite earlier
+ * ones' entries.  Process-wide; off by default (then it costs one uniform
+ * branch per workgroup). */
+T0G_API int t0g_set_timeline(int on);
+/* Copy the first `entries` u64 of the device's timeline array (4 per workgroup)
+ * to out, after the device stream has drained; *written: how many were copied
+ * (at most 4 * 8192). */
+T0G_API int t0g_timeline_read(t0g_device *dev, uint64_t *out, size_t entries, size_t *written);
+/* Zero the device's timeline array (entries of workgroups that did not run stay 0). */
+T0G_API int t0g_timeline_clear(t0g_device *dev);
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
  * real device fault. */

@@ -57,6 +57,49 @@ __device__ __forceinline__ uint32_t lds_off(uint32_t row, uint32_t chunk) {
 
 __device__ __forceinline__ u32x4_t zero4() { return u32x4_t{0u, 0u, 0u, 0u}; }
 
+// Workgroup timeline (T0G_FLAG_TIMELINE), a diagnostic: built only into the
+// second code object (T0G_TIMELINE defined), which the runtime launches while
+// the host has the timeline switched on.  The fast kernels then record, per
+// linear workgroup id, the constant 100 MHz clock at entry, after the K loop
+// and after the epilogue's stores have completed, plus the XCC and hardware
+// ids of the recording wave; the host reads the array with
+// hipModuleGetGlobal.  The production code object carries none of it: even
+// switched off, the marks moved the 4-wave 256x256 kernel's 11008x4096x1024
+// launch by 2-5 %.
+#ifdef T0G_TIMELINE
+}  // namespace t0g
+extern "C" {
+__device__ __attribute__((aligned(256))) uint64_t t0g_timeline[T0G_TIMELINE_SLOTS * 4];
+}
+namespace t0g {
+#endif
+
+// Entry `ev` (0: entry, 1: end of the K loop, 2: stores completed, which also
+// writes the ids) of this workgroup's record, written as it happens so that no
+// clock value is held in registers across the K loop.
+__device__ __forceinline__ void tl_mark(const T0gGemmArgs& p, int ev) {
+#ifndef T0G_TIMELINE
+    (void)p;
+    (void)ev;
+#else
+    if (p.flags & T0G_FLAG_TIMELINE) {
+        if (ev == 2) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the epilogue's stores have completed
+        const uint64_t t = __builtin_amdgcn_s_memrealtime();
+        const uint32_t slot = blockIdx.y * gridDim.x + blockIdx.x;
+        if (threadIdx.x == 0 && slot < T0G_TIMELINE_SLOTS) {
+            uint64_t* e = t0g_timeline + (uint64_t)slot * 4;
+            e[ev] = t;
+            if (ev == 2) {
+                // XCC_ID is hardware register 20 on gfx950 (bits 3:0), HW_ID register 4
+                const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;
+                const uint32_t hw = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+                e[3] = ((uint64_t)xcc << 32) | hw;
+            }
+        }
+    }
+#endif
+}
+
 __device__ __forceinline__ u32x4_t pack8(const uint16_t e[8]) {
     return u32x4_t{(uint32_t)e[0] | ((uint32_t)e[1] << 16), (uint32_t)e[2] | ((uint32_t)e[3] << 16),
                    (uint32_t)e[4] | ((uint32_t)e[5] << 16), (uint32_t)e[6] | ((uint32_t)e[7] << 16)};
@@ -1013,6 +1056,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
     constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
     __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE];
 
+    tl_mark(p, 0);
     const uint32_t tid = threadIdx.x;
     const GridPos gp = grid_pos(p);
     const uint32_t bid = gp.tile;
@@ -1063,6 +1107,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
     static_assert((NT / 64) * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
     T0G_WAIT_VMCNT(0);    // LDS DMA still in flight (stages past K) has landed
     barrier_no_fence();   // and every wave is done with the ring
+    tl_mark(p, 1);
     if constexpr (RED) {
         // the partial tile, raw fp32, row-major into this workgroup's slot
         T0gGemmArgs q = p;
@@ -1081,6 +1126,7 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
         store_tile_vec<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
                                          lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, vec, gp.split);
     }
+    tl_mark(p, 2);
 }
 
 // Plane-ordered split-K reduction: y = ((0 + p0) + p1) + ... in fp32, the

@@ -645,6 +645,7 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p, const T0g
     constexpr int kVmemPerStage = OpA::kInstr + OpB::kInstr;
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
+    tl_mark(p, 0);
     const uint32_t tid = threadIdx.x;
     uint32_t m0, n0;
     tile_origin<BM, BN>(p, m0, n0);
@@ -689,6 +690,7 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p, const T0g
     mfma16_drain();
     T0G_WAIT_VMCNT(0);
     barrier_no_fence();
+    tl_mark(p, 1);
     if constexpr (RED) {
         red_store_and_finish<BM, BN, NT, SM, SN, OUT_BF16>(p, *ra, acc, wm * WTM, wn * WTN, lane, wave, m0, n0,
                                                            lds_addr(smem), 2 * STAGE);
@@ -697,6 +699,7 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p, const T0g
         store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
                                            lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
     }
+    tl_mark(p, 2);
 }
 
 
@@ -786,6 +789,7 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p, const T0gGemm
     constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
+    tl_mark(p, 0);
     const uint32_t tid = threadIdx.x;
     uint32_t m0, n0;
     tile_origin<BM, BN>(p, m0, n0);
@@ -829,6 +833,7 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p, const T0gGemm
     mfma16_drain();
     T0G_WAIT_VMCNT(0);
     barrier_no_fence();
+    tl_mark(p, 1);
     if constexpr (RED) {
         red_store_and_finish<BM, BN, NT, SM, SN, OUT_BF16>(p, *ra, acc, wm * WTM, wn * WTN, lane, wave, m0, n0,
                                                            lds_addr(smem), 2 * STAGE);
@@ -837,6 +842,7 @@ __device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p, const T0gGemm
         store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
                                            lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
     }
+    tl_mark(p, 2);
 }
 
 // ---- stream-K ------------------------------------------------------------------

@@ -130,6 +130,11 @@ typedef struct T0gConvertArgs {
 #define T0G_FLAG_XCD_REMAP 1u   /* remap workgroup ids so each XCD owns a contiguous tile (128x128, 64x64: (split, tile)) range */
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
 #define T0G_FLAG_BIAS 4u        /* the chain reads bias[col]                                     */
+#define T0G_FLAG_TIMELINE 8u    /* record the workgroup's timeline in t0g_timeline (diagnostics)   */
+/* t0g_timeline: T0G_TIMELINE_SLOTS entries of 4 u64 per linear workgroup id: clock at entry, at
+ * the end of the K loop and after the epilogue's stores completed (s_memrealtime, 100 MHz),
+ * then XCC_ID << 32 | HW_ID of the wave that wrote it. */
+#define T0G_TIMELINE_SLOTS 8192u
 #define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
 #define T0G_REDUCE_BIAS 2u      /* the chain reads bias[col]                                     */
 #define T0G_REDUCE_VEC8 4u      /* planes 32-byte aligned, N % 8 == 0, C rows aligned for 8 elements */

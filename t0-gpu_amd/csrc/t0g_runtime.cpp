@@ -38,6 +38,17 @@ __asm__(".section .rodata.t0g_hsaco,\"a\",@progbits\n"
         ".previous\n");
 extern "C" const unsigned char t0g_hsaco_begin[];
 extern "C" const unsigned char t0g_hsaco_end[];
+// The same kernels with the workgroup timeline compiled in (T0G_HSACO_TL_FILE),
+// loaded on a device the first time the timeline is used there.
+__asm__(".section .rodata.t0g_hsaco_tl,\"a\",@progbits\n"
+        ".p2align 12\n"
+        ".hidden t0g_hsaco_tl_begin\n"
+        ".globl t0g_hsaco_tl_begin\n"
+        "t0g_hsaco_tl_begin:\n"
+        ".incbin \"" T0G_HSACO_TL_FILE "\"\n"
+        ".byte 0\n"
+        ".previous\n");
+extern "C" const unsigned char t0g_hsaco_tl_begin[];
 
 namespace t0g {
 
@@ -63,10 +74,12 @@ struct t0g_device {
     hipStream_t stream = nullptr;
     hipEvent_t order_event = nullptr;   // orders launches across t0g_device_set_stream
     hipModule_t module = nullptr;
+    hipModule_t module_tl = nullptr;   // the timeline build of the same kernels (loaded on first use)
     std::mutex mu;
     bool poisoned = false;
     std::string poison_reason;
     std::unordered_map<std::string, hipFunction_t> fns;
+    std::unordered_map<std::string, hipFunction_t> fns_tl;
     std::vector<std::unique_ptr<t0g_kernel>> kernels;
     std::unordered_map<std::string, t0g_kernel *> kernel_cache;
     std::vector<hipModule_t> extra_modules;
@@ -106,6 +119,8 @@ static std::atomic<uint32_t> g_sk_debug{0};
 // Split-K: 0 = reduce inside the GEMM kernel where the plan allows it (the _r
 // kernels), 1 = always partial planes plus the separate reduce kernel.
 static std::atomic<uint32_t> g_split_mode{T0G_SPLIT_K_REDUCE_KERNEL};
+// Workgroup timeline recording (t0g_set_timeline): a diagnostic, off by default.
+static std::atomic<int> g_timeline{0};
 // Polls a workgroup of a fused split-K launch waits for its tile's other K
 // slices before leaving its chunk to the tile's last arrival (a few tens of
 // microseconds: within one wave of workgroups the slices finish together).
@@ -186,16 +201,32 @@ static int wait_stream(t0g_device *dev) {
     }
 }
 
-static int get_function(t0g_device *dev, const std::string &name, hipFunction_t *out) {
-    auto it = dev->fns.find(name);
-    if (it != dev->fns.end()) {
+static int load_timeline_module(t0g_device *dev) {
+    if (dev->module_tl) return T0G_OK;
+    hipError_t e = T0G_HIP(hipModuleLoadData(&dev->module_tl, t0g_hsaco_tl_begin));
+    if (e != hipSuccess) {
+        dev->module_tl = nullptr;
+        return hip_fail(e, "hipModuleLoadData(timeline code object)");
+    }
+    return T0G_OK;
+}
+
+// timeline: the kernel from the timeline build of the code object.
+static int get_function(t0g_device *dev, const std::string &name, hipFunction_t *out, bool timeline = false) {
+    auto &fns = timeline ? dev->fns_tl : dev->fns;
+    auto it = fns.find(name);
+    if (it != fns.end()) {
         *out = it->second;
         return T0G_OK;
     }
+    if (timeline) {
+        int rc = load_timeline_module(dev);
+        if (rc) return rc;
+    }
     hipFunction_t f = nullptr;
-    hipError_t e = T0G_HIP(hipModuleGetFunction(&f, dev->module, name.c_str()));
+    hipError_t e = T0G_HIP(hipModuleGetFunction(&f, timeline ? dev->module_tl : dev->module, name.c_str()));
     if (e != hipSuccess) return hip_fail(e, ("hipModuleGetFunction(" + name + ")").c_str());
-    dev->fns.emplace(name, f);
+    fns.emplace(name, f);
     *out = f;
     return T0G_OK;
 }
@@ -402,7 +433,7 @@ static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws
     args.tiles_m = p.tiles_m;
     args.tiles_n = p.tiles_n;
     args.group_m = 8;
-    args.flags = T0G_FLAG_XCD_REMAP;
+    args.flags = T0G_FLAG_XCD_REMAP | (g_timeline.load() ? T0G_FLAG_TIMELINE : 0u);
     const bool reduce = p.splits > 1 && o.c_split_stride == 0 && !p.fused;
     if (reduce) {
         args.c = ws;
@@ -429,12 +460,12 @@ static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws
 // Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
 // the partial planes go to `ws` and the reduce kernel produces C.
 static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws) {
-    hipFunction_t f = nullptr;
-    int rc = get_function(dev, p.symbol, &f);
-    if (rc) return rc;
     T0gGemmArgs args;
     bool reduce = false;
     fill_gemm_args(p, o, ws, &args, &reduce);
+    hipFunction_t f = nullptr;
+    int rc = get_function(dev, p.symbol, &f, (args.flags & T0G_FLAG_TIMELINE) != 0);
+    if (rc) return rc;
     if (p.fused) {
         T0gGemmRedArgs ra;
         memset(&ra, 0, sizeof ra);
@@ -612,6 +643,52 @@ int t0g_set_split_k_mode(uint32_t mode) {
     return ok();
 }
 
+int t0g_set_timeline(int on) {
+    g_timeline.store(on ? 1 : 0);
+    return ok();
+}
+
+// The module's t0g_timeline array (device address and size).
+static int timeline_global(t0g_device *dev, hipDeviceptr_t *ptr, size_t *bytes) {
+    int rc = load_timeline_module(dev);
+    if (rc) return rc;
+    hipError_t e = T0G_HIP(hipModuleGetGlobal(ptr, bytes, dev->module_tl, "t0g_timeline"));
+    if (e != hipSuccess) return hip_fail(e, "hipModuleGetGlobal(t0g_timeline)");
+    return T0G_OK;
+}
+
+int t0g_timeline_read(t0g_device *dev, uint64_t *out, size_t entries, size_t *written) {
+    if (!dev || !written || (!out && entries)) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *written = 0;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipDeviceptr_t p = nullptr;
+    size_t bytes = 0;
+    if ((rc = timeline_global(dev, &p, &bytes))) return rc;
+    const size_t n = entries < bytes / 8 ? entries : bytes / 8;
+    if ((rc = wait_stream(dev))) return rc;   // the recorded launches have finished
+    hipError_t e = T0G_HIP(hipMemcpyAsync(out, p, n * 8, hipMemcpyDeviceToHost, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemcpy D2H (timeline)"));
+    if ((rc = wait_stream(dev))) return rc;
+    *written = n;
+    return ok();
+}
+
+int t0g_timeline_clear(t0g_device *dev) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    hipDeviceptr_t p = nullptr;
+    size_t bytes = 0;
+    if ((rc = timeline_global(dev, &p, &bytes))) return rc;
+    hipError_t e = T0G_HIP(hipMemsetAsync(p, 0, bytes, dev->stream));
+    if (e != hipSuccess) return poison(dev, hip_fail(e, "hipMemset (timeline)"));
+    if ((rc = wait_stream(dev))) return rc;
+    return ok();
+}
+
 int t0g_device_count(int *count) {
     if (!count) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
     int n = 0;
@@ -681,6 +758,7 @@ int t0g_device_close(t0g_device *dev) {
         for (uint64_t a : bucket.second) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
     if (dev->module) (void)hipModuleUnload(dev->module);
+    if (dev->module_tl) (void)hipModuleUnload(dev->module_tl);
     if (dev->order_event) (void)hipEventDestroy(dev->order_event);
     if (dev->own_stream) (void)hipStreamDestroy(dev->own_stream);
     delete dev;

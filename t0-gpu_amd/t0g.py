@@ -318,6 +318,10 @@ _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 _sig("t0g_set_stream_k_spin_limit", ctypes.c_int, _u32)
 _sig("t0g_debug_stream_k_stall", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_split_k_mode", ctypes.c_int, _u32)
+_sig("t0g_set_timeline", ctypes.c_int, ctypes.c_int)
+_sig("t0g_timeline_read", ctypes.c_int, _p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
+     ctypes.POINTER(ctypes.c_size_t))
+_sig("t0g_timeline_clear", ctypes.c_int, _p)
 
 
 def _check(rc):
@@ -522,6 +526,15 @@ def set_split_k_mode(mode):
     _check(_lib.t0g_set_split_k_mode(mode))
 
 
+TIMELINE_SLOTS = 8192
+TIMELINE_TICK_NS = 10.0   # the GPU's constant 100 MHz clock
+
+
+def set_timeline(on):
+    """Record per-workgroup timelines of later GEMM launches (diagnostic)."""
+    _check(_lib.t0g_set_timeline(1 if on else 0))
+
+
 def debug_fail_hip_call(n):
     _check(_lib.t0g_debug_fail_hip_call(n))
 
@@ -662,6 +675,20 @@ class GpuRuntime:
         addr = self.alloc(arr.nbytes)
         self.write(addr, arr)
         return addr
+
+    def timeline_clear(self):
+        _check(_lib.t0g_timeline_clear(self.handle))
+
+    def timeline_read(self, workgroups=TIMELINE_SLOTS):
+        """[workgroups][4] uint64: clock at entry, after the K loop, after the stores
+        (ticks of TIMELINE_TICK_NS), then XCC_ID << 32 | HW_ID; rows of workgroups
+        that did not run are zero."""
+        import numpy as np
+        out = np.zeros((workgroups, 4), dtype=np.uint64)
+        n = ctypes.c_size_t()
+        _check(_lib.t0g_timeline_read(self.handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                                      out.size, ctypes.byref(n)))
+        return out
 
     def memset(self, addr, value, nbytes):
         _check(_lib.t0g_memset(self.handle, addr, value, nbytes))

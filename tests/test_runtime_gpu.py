@@ -453,3 +453,50 @@ def test_tune_tile_ir_on_the_thin_shape(rt, tmp_path):
     finally:
         for a in (xa, wa, y):
             rt.free(a)
+
+
+# ---- workgroup timeline (diagnostic) -------------------------------------------
+
+@pytest.mark.parametrize("preset,m,n,k,sk,layout", [
+    ("tile_256x256_k64", 1024, 768, 512, 0, "NN"),      # 12 workgroups, 8-wave ping-pong kernel
+    ("tile_256x256_k64", 512, 768, 384, 0, "NT"),       # 6 workgroups, 8-wave ping-pong kernel
+    ("tile_256x256_k64", 512, 512, 384, 0, "TN"),       # 4 workgroups, 4-wave kernel
+    ("tile_128x128_k64", 256, 640, 1024, 4, "NT"),      # 10 tiles x 4 K slices, deep-ring kernel
+    ("tile_64x64_k64", 1024, 1024, 128, 0, "NN"),       # 256 workgroups, 4-stage ring kernel
+])
+def test_timeline_records_every_workgroup(rt, preset, m, n, k, sk, layout):
+    """With t0g_set_timeline on, launches run the instrumented build of the kernels
+    and each workgroup leaves one entry: entry clock <= end of its K loop <= its
+    stores completed, an XCD id below 8; the result is unchanged.  Off again, the
+    production kernels run and record nothing."""
+    _log(f"[case] timeline {preset} {m}x{n}x{k} sk={sk} {layout}")
+    a_mk = o.rand_bf16_lcg(m * k, 31 + m).reshape(m, k)
+    b_nk = o.rand_bf16_lcg(n * k, 37 + n).reshape(n, k)
+    a = rt.upload(a_mk if layout[0] == "N" else np.ascontiguousarray(a_mk.T))
+    b = rt.upload(b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T))
+    c = rt.alloc(m * n * 4)
+    cfg = t0g.GemmConfig.preset(preset)
+    d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, config=cfg, split_k=sk)
+    tile = cfg.tile_m
+    wgs = ((m + tile - 1) // tile) * ((n + tile - 1) // tile) * max(sk, 1)
+    try:
+        rt.timeline_clear()
+        t0g.set_timeline(True)
+        rt.gemm_desc(d)
+        rt.wait_idle()
+        tl = rt.timeline_read()
+    finally:
+        t0g.set_timeline(False)
+    rows = tl[tl[:, 0] != 0]
+    assert len(rows) == wgs and not tl[wgs:].any(), f"{len(rows)} entries for {wgs} workgroups"
+    assert np.all(rows[:, 0] <= rows[:, 1]) and np.all(rows[:, 1] <= rows[:, 2])
+    assert np.all((rows[:, 3] >> np.uint64(32)) < 8)
+    span_us = (rows[:, 2].max() - rows[:, 0].min()) * t0g.TIMELINE_TICK_NS / 1e3
+    assert 0 < span_us < 1e5
+    check_parity(rt.read(c, (m, n), np.float32), o.gemm("NT", a_mk, b_nk, m, n, k), k, f"timeline {preset}")
+    rt.timeline_clear()
+    rt.gemm_desc(d)
+    rt.wait_idle()
+    assert not rt.timeline_read().any(), "a launch with the timeline off recorded entries"
+    for x in (a, b, c):
+        rt.free(x)
