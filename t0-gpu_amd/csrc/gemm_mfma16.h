@@ -425,17 +425,24 @@ __device__ __forceinline__ void store_tile_bf16_tr(const T0gGemmArgs& p, const f
         // one band at a time
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t reg = lds + (uint32_t)(i & 1) * kRegion;
+        // the band's SN x 4 values through the chain at once (the chain is decoded
+        // once per band)
+        float v[SN * 4], b4[SN * 4];
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[4 * j + r] = acc_read(acc[i][j][r]);
+                b4[4 * j + r] = bv[j];
+            }
+        apply_epilogue_n<SN * 4>(v, b4, ep);
 #pragma unroll
         for (int j = 0; j < SN; ++j) {
-            float v[4] = {acc_read(acc[i][j][0]), acc_read(acc[i][j][1]), acc_read(acc[i][j][2]),
-                          acc_read(acc[i][j][3])};
-            const float b4[4] = {bv[j], bv[j], bv[j], bv[j]};
-            apply_epilogue_n<4>(v, b4, ep);
             u32x2_t w;
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                w[h] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * h]) |
-                       ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * h + 1]) << 16);
+                w[h] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[4 * j + 2 * h]) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[4 * j + 2 * h + 1]) << 16);
             *reinterpret_cast<lds_u32x2*>((uintptr_t)(reg + bf16_stage_off(16u * j + l16, q))) = w;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
