@@ -177,13 +177,28 @@ def num_threads():
     return _lib.oracle_num_threads()
 
 
+# Entries whose reference magnitude is below 2^-100 are judged by max|d| alone.
+# The hardware exp2 and reciprocal of the SiLU/GELU epilogue (v_exp_f32,
+# v_rcp_f32: the instructions the reference emits, src/t0/tile_ir.rs:2270-2317)
+# flush subnormal results, so x * rcp(1 + exp(-x)) is 0 on the device where the
+# fp32 CPU expectation keeps a subnormal reciprocal: for x near -88 the two
+# differ by up to |x| * 2^-126 ~ 1e-36.  A matrix made only of such values
+# (the reference's LCG inputs are all <= 0, so every GEMM output of a long K is
+# positive and [silu, scale < 0, silu] sends all of them there) would otherwise
+# fail relF on differences of 1e-36.
+RELF_FLOOR = 2.0 ** -100
+
+
 def parity(c_gpu, c_ref, k):
-    """The north-star gate: relF <= 5e-3 and max|d| <= 1e-2 * sqrt(K/256).  Returns (ok, relF, maxabs, bound)."""
+    """The north-star gate: relF <= 5e-3 and max|d| <= 1e-2 * sqrt(K/256).  Returns (ok, relF, maxabs, bound).
+
+    relF is taken over the entries with |ref| >= RELF_FLOOR; the others count in max|d| only."""
     c_gpu = np.asarray(c_gpu, dtype=np.float64)
     c_ref = np.asarray(c_ref, dtype=np.float64)
     diff = c_gpu - c_ref
-    nref = np.linalg.norm(c_ref)
-    relf = float(np.linalg.norm(diff) / nref) if nref > 0 else float(np.linalg.norm(diff))
+    big = np.abs(c_ref) >= RELF_FLOOR
+    nref = np.linalg.norm(c_ref[big])
+    relf = float(np.linalg.norm(diff[big]) / nref) if nref > 0 else 0.0
     maxabs = float(np.max(np.abs(diff))) if diff.size else 0.0
     bound = 1e-2 * np.sqrt(max(k, 1) / 256.0)
     return (relf <= 5e-3 and maxabs <= bound), relf, maxabs, bound

@@ -207,6 +207,27 @@ def test_parity_gate_rejects_wrong_results():
     assert not o.parity(c.T.copy(), c, k)[0]
 
 
+def test_parity_gate_subnormal_regime():
+    """Entries below 2^-100 count in max|d| only: a device result that flushes a
+    subnormal reciprocal passes, an error in ordinary values still fails, and a
+    tiny value in the place of an ordinary one fails through relF."""
+    x = np.linspace(-84.0, -88.5, 4096).astype(np.float32).reshape(64, 64)   # exp(-x) < FLT_MAX
+    ref = o.epilogue_chain(x, ["silu"])                 # CPU fp32, subnormal reciprocals kept
+    assert np.abs(ref).max() < 1e-34 and (np.abs(ref) >= 2.0 ** -126).all()
+    e = np.exp(np.float32(-1.0) * x.astype(np.float64))
+    flushed = np.where(1.0 / (1.0 + e) < 2.0 ** -126, 0.0, ref).astype(np.float32)
+    assert (flushed == 0).any() and o.parity(flushed, ref, 256)[0]
+    mixed_ref = ref.copy()
+    mixed_ref[0, :8] = 1.0
+    assert o.parity(flushed.copy() + (mixed_ref - ref), mixed_ref, 256)[0]
+    wrong = mixed_ref.copy()
+    wrong[0, 3] = 1.02                                  # 2 % off in an ordinary entry
+    assert not o.parity(wrong, mixed_ref, 256)[0]
+    dropped = mixed_ref.copy()
+    dropped[0, :8] = 1e-35                              # ordinary values replaced by tiny ones
+    assert not o.parity(dropped, mixed_ref, 256)[0]
+
+
 def test_epilogue_chain_known_answers():
     """Each epilogue op against values fixed by the mathematics (not by retyping the
     oracle's formulas): exact results for the piecewise ops, the identity

@@ -20,7 +20,12 @@ import t0g
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 48
+import os
+
+# T0G_SWEEP_CASES / T0G_SWEEP_SEED0: a longer sweep, or another slice of seeds, for
+# one-off correctness runs; the default is the committed 48-case sweep.
+N_CASES = int(os.environ.get("T0G_SWEEP_CASES", "48"))
+SEED0 = int(os.environ.get("T0G_SWEEP_SEED0", "1000"))
 PRESETS = [None, "tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
 
 
@@ -37,7 +42,7 @@ def rt():
 
 
 def _case(i):
-    rng = np.random.default_rng(1000 + i)
+    rng = np.random.default_rng(SEED0 + i)
     layout = ["NT", "NN", "TN", "TT"][i % 4]
     m = int(rng.integers(1, 701))
     n = int(rng.integers(1, 701))
