@@ -1426,6 +1426,23 @@ T0G_GEMM_TILE_U(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_D(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_D(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 
+// Deep-ring kernels with the split-K reduced inside the kernel (suffix _dr).
+#define T0G_GEMM_DR(NAME, BM, BN, WM, WN, AK, BKM, OBF)                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))       \
+        NAME(T0gGemmRedArgs ra) {                                                                              \
+        t0g::gemm_tile_fast<BM, BN, WM, WN, AK, BKM, OBF, T0G_PIPE_D_##BM##x##BN, true>(ra.g, &ra);             \
+    }
+#define T0G_GEMM_LAYOUTS_DR(PFX, BM, BN, WM, WN, OUTN, OBF)                  \
+    T0G_GEMM_DR(PFX##_nt_##OUTN##_dr, BM, BN, WM, WN, true, true, OBF)       \
+    T0G_GEMM_DR(PFX##_nn_##OUTN##_dr, BM, BN, WM, WN, true, false, OBF)      \
+    T0G_GEMM_DR(PFX##_tn_##OUTN##_dr, BM, BN, WM, WN, false, false, OBF)     \
+    T0G_GEMM_DR(PFX##_tt_##OUTN##_dr, BM, BN, WM, WN, false, true, OBF)
+#define T0G_GEMM_TILE_DR(PFX, BM, BN, WM, WN)                \
+    T0G_GEMM_LAYOUTS_DR(PFX, BM, BN, WM, WN, f32, false)     \
+    T0G_GEMM_LAYOUTS_DR(PFX, BM, BN, WM, WN, bf16, true)
+T0G_GEMM_TILE_DR(t0g_gemm_64x64_k64, 64, 64, 2, 2)
+T0G_GEMM_TILE_DR(t0g_gemm_128x128_k64, 128, 128, 2, 2)
+
 extern "C" __global__ void __launch_bounds__(256) t0g_splitk_reduce_f32(T0gReduceArgs p) {
     t0g::splitk_reduce<false>(p);
 }

@@ -333,19 +333,21 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     p->splits = sk;
     p->k_per_split = kps;
     const bool partial = sk > 1;
-    // In-kernel reduction: 128x128 and 256x256 tiles, a power-of-two split (the
-    // tile is summed in splits equal chunks), one wave of workgroups (a slice
-    // waits only for slices running at the same time) and slots addressable
-    // by a 32-bit buffer descriptor.
-    const uint64_t red_grid = (uint64_t)p->tiles_m * p->tiles_n * sk;
-    p->fused = partial && allow_fused && g_split_mode.load() == T0G_SPLIT_K_IN_KERNEL && aligned && !wide && !stream_k &&
-               (tile->bm == 256 || tile->bm == 128) && (sk & (sk - 1)) == 0 && sk <= kMaxSplitK &&
-               red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
-               red_grid * tile->bm * tile->bn * 4 < (1ull << 31);
     // At most one workgroup per CU: the 64x64 and 128x128 tiles switch to their
     // deep-ring variants (the CU's LDS then holds one workgroup with 128 KB of
     // 64-K stages, whole cache lines per DMA request).
-    const bool deep = tile_uses_deep(*tile, (uint64_t)p->tiles_m * p->tiles_n * sk) && aligned && !wide && !p->fused;
+    const uint64_t red_grid = (uint64_t)p->tiles_m * p->tiles_n * sk;
+    const bool deep = tile_uses_deep(*tile, red_grid) && aligned && !wide;
+    // In-kernel reduction: a power-of-two split whose chunks (the tile cut in
+    // `splits` equal parts) hold 256 elements or more, one wave of workgroups
+    // (a slice waits only for slices running at the same time) and slots
+    // addressable by a 32-bit buffer descriptor.  The 64x64 tile has it in its
+    // deep-ring kernel only.
+    p->fused = partial && allow_fused && g_split_mode.load() == T0G_SPLIT_K_IN_KERNEL && aligned && !wide && !stream_k &&
+               (tile->bm != 64 || deep) && (sk & (sk - 1)) == 0 && sk <= kMaxSplitK &&
+               (uint64_t)sk * 256 <= (uint64_t)tile->bm * tile->bn &&
+               red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
+               red_grid * tile->bm * tile->bn * 4 < (1ull << 31);
     // The 256x256 kernels with a K-contiguous A (NN, NT) run 8 waves in
     // ping-pong; with an M-contiguous A (TN, TT) every fragment is a transposed
     // LDS read and the 4-wave kernel, with half the fragment reads per CU, is
@@ -353,7 +355,7 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
                 ((out_bf16 && (!partial || p->fused)) ? "bf16" : "f32") +
-                (aligned ? (wide ? "_x" : deep ? "_d" : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");
+                (aligned ? (wide ? "_x" : deep ? (p->fused ? "_dr" : "_d") : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
     if (stream_k && (uint64_t)p->tiles_m * p->tiles_n * p->sk_ipt > 0x7FFFFFFFull)

@@ -80,7 +80,7 @@ def test_argument_block_sizes_match_the_header(blob):
                     names.add(part[:-3].decode())
     assert len(names) >= 60
     for s in sorted(names):
-        want = 144 if s.endswith("_sk") or s.endswith("_r") else 104   # T0gGemmSkArgs / T0gGemmRedArgs
+        want = 144 if s.endswith(("_sk", "_r", "_dr")) else 104   # T0gGemmSkArgs / T0gGemmRedArgs
         assert t0g.code_object_kernel_meta(blob, s).kernarg_size == want, s
 
 

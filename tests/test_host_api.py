@@ -157,17 +157,24 @@ def test_gemm_plan_selection_host_only():
 
 def test_split_k_mode_selects_the_reduction():
     """By default split-K writes fp32 planes for the reduce kernel; the in-kernel mode
-    takes the _r kernel (which writes the output dtype and sums the planes itself),
-    and only where its plan conditions hold; an unknown mode is refused."""
-    def name(**kw):
-        return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 128, 4096, 4096, transpose="NT",
+    takes the _r kernel, or _dr where the grid runs the deep-ring kernel (both write
+    the output dtype and sum the planes themselves), and only where its plan
+    conditions hold; an unknown mode is refused."""
+    def name(m=128, n=4096, **kw):
+        return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, m, n, 4096, transpose="NT",
                                                   out_dtype=t0g.BF16, **kw))
     c128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    c64 = t0g.GemmConfig.preset("tile_64x64_k64")
     # 32 tiles x 8 slices: one workgroup per CU, so the deep-ring kernel writes the planes
     assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
     t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
     try:
-        assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_r"
+        assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_dr"
+        assert name(m=256, config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_r"   # 512 workgroups
+        assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_bf16_dr"
+        assert name(config=c64, split_k=16) == "t0g_gemm_64x64_k64_nt_f32"       # 2048 workgroups: no _r kernel
+        assert name(m=64, n=512, config=c64, split_k=16) == "t0g_gemm_64x64_k64_nt_bf16_dr"
+        assert name(m=64, n=512, config=c64, split_k=32) == "t0g_gemm_64x64_k64_nt_f32_d"   # 128-element chunks
         assert name(config=c128, split_k=6) == "t0g_gemm_128x128_k64_nt_f32_d"   # not a power of two
         assert name(config=c128) == "t0g_gemm_128x128_k64_nt_bf16_d"              # no split, nothing to sum
         with pytest.raises(t0g.T0gError) as e:

@@ -1,12 +1,13 @@
-"""Split-K reduced inside the GEMM kernel (the _r kernels), through the C ABI.
+"""Split-K reduced inside the GEMM kernel (the _r and _dr kernels), through the C ABI.
 
 The in-kernel reduction sums every chunk of a tile over its K slices in plane
 order from 0.0, the order of the separate reduce kernel and of the reference's
 host loop (examples/test_gemm_correctness.rs:190-207).  So each case runs once
 reduced in the kernel and once as planes plus the reduce kernel
 (t0g_set_split_k_mode) and the two outputs must be identical bit for bit; the
-result is also checked against the oracle.  Cases cover both tiles that have an
-in-kernel form (128x128, 256x256 in its 8-wave and 4-wave kernels), all
+result is also checked against the oracle.  Cases cover every kernel that has an
+in-kernel form (128x128, 256x256 in its 8-wave and 4-wave kernels, the 64x64
+and 128x128 deep-ring kernels of grids with one workgroup per CU), all
 layouts, f32 and bf16 output, ragged M/N edges, K tails, epilogue chains,
 repeated launches (the control words must be back at zero after each) and the
 host-forced path in which every workgroup but a tile's last arrival gives up
@@ -23,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 P128 = t0g.GemmConfig.preset("tile_128x128_k64")
 P256 = t0g.GemmConfig.preset("tile_256x256_k64")
+P64 = t0g.GemmConfig.preset("tile_64x64_k64")
 
 
 def _log(msg):
@@ -81,6 +83,11 @@ CASES = [
     ("TN", 200, 296, 4096, P128, 4),       # ragged M and N on 128x128
     ("NN", 320, 136, 3000, P128, 4),       # K tail: 3000 in slices of 768
     ("TT", 128, 128, 8192, P128, 32),      # a single tile in 32 slices
+    ("NT", 128, 4096, 4096, P64, 2),       # benchmark config 4a on the 64x64 deep-ring kernel
+    ("NT", 256, 256, 32768, P64, 16),      # benchmark config 4b: 16 slices, 256-element chunks
+    ("NN", 192, 320, 5000, P64, 4),        # K tail on the 64x64 deep-ring kernel
+    ("TN", 104, 200, 3000, P64, 8),        # ragged M and N, M-contiguous A (rows of 16-byte multiples)
+    ("TT", 64, 64, 4096, P64, 16),         # a single 64x64 tile in 16 slices
 ]
 
 
@@ -93,7 +100,9 @@ def test_fused_equals_reduce_kernel(rt, layout, m, n, k, cfg, sk, out):
     try:
         name_f, fused = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_IN_KERNEL)
         name_r, planes = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_REDUCE_KERNEL)
-        assert name_f.endswith("_r") and not name_r.endswith("_r"), (name_f, name_r)
+        assert name_f.endswith(("_r", "_dr")) and not name_r.endswith(("_r", "_dr")), (name_f, name_r)
+        assert name_f.endswith("_dr") == (cfg.tile_m < 256 and (m + cfg.tile_m - 1) // cfg.tile_m *
+                                          ((n + cfg.tile_n - 1) // cfg.tile_n) * sk <= 256), name_f
         assert np.array_equal(fused, planes), f"{name_f} differs from planes + reduce kernel"
         got = fused if out == t0g.F32 else o.bf16_to_f32(fused)
         ok, relf, maxabs, bound = o.parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k)
@@ -104,7 +113,7 @@ def test_fused_equals_reduce_kernel(rt, layout, m, n, k, cfg, sk, out):
         rt.free(db)
 
 
-@pytest.mark.parametrize("layout,m,n,k,cfg,sk", [CASES[0], CASES[3], CASES[7]])
+@pytest.mark.parametrize("layout,m,n,k,cfg,sk", [CASES[0], CASES[3], CASES[7], CASES[9], CASES[12]])
 def test_fused_epilogue_chain(rt, layout, m, n, k, cfg, sk):
     """bias + SiLU + clamp applied once, after the sum (not per slice)."""
     a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 7 + n)
@@ -135,11 +144,12 @@ def test_fused_epilogue_chain(rt, layout, m, n, k, cfg, sk):
             rt.free(x)
 
 
-def test_fused_repeated_launches_and_stall(rt):
+@pytest.mark.parametrize("case", [0, 9, 10])
+def test_fused_repeated_launches_and_stall(rt, case):
     """Eight launches back to back give the same bits (the arrival and claim words
     are reset by every launch); with the host-forced stall every tile is summed by
     its last arrival alone, with the same bits; no launch counts a timeout."""
-    layout, m, n, k, cfg, sk = CASES[0]
+    layout, m, n, k, cfg, sk = CASES[case]
     a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 55)
     da, db = rt.upload(a_st), rt.upload(b_st)
     try:
