@@ -9,9 +9,10 @@ result is also checked against the oracle.  Cases cover every kernel that has an
 in-kernel form (128x128, 256x256 in its 8-wave and 4-wave kernels, the 64x64
 and 128x128 deep-ring kernels of grids with one workgroup per CU), all
 layouts, f32 and bf16 output, ragged M/N edges, K tails, epilogue chains,
-repeated launches (the control words must be back at zero after each) and the
+repeated launches (the control words must be back at zero after each), the
 host-forced path in which every workgroup but a tile's last arrival gives up
-waiting, so the last arrival sums the whole tile."""
+waiting, so the last arrival sums the whole tile, and a seeded sweep of random
+aligned problems (24 committed; 400 pass with T0G_FUSED_SWEEP_CASES=400)."""
 import sys
 
 import numpy as np
@@ -164,6 +165,40 @@ def test_fused_repeated_launches_and_stall(rt, case):
         assert np.array_equal(once, alone)
         assert rt.stream_k_timeouts() == 0
         assert not rt.is_poisoned()
+    finally:
+        rt.free(da)
+        rt.free(db)
+
+
+# T0G_FUSED_SWEEP_CASES: a longer run of the seeded sweep below for one-off checks.
+N_SWEEP = int(__import__("os").environ.get("T0G_FUSED_SWEEP_CASES", "24"))
+
+
+@pytest.mark.parametrize("i", range(N_SWEEP))
+def test_fused_random_problem(rt, i):
+    """Seeded random problems whose rows are 16-byte aligned (so the in-kernel form
+    applies wherever its grid conditions hold): layout, M, N, K, tile, a power-of-two
+    split, both outputs.  The in-kernel result must equal planes + reduce kernel bit
+    for bit and pass the oracle gate."""
+    rng = np.random.default_rng(7000 + i)
+    layout = ["NT", "NN", "TN", "TT"][i % 4]
+    cfg = [P64, P128, P256][int(rng.integers(0, 3))]
+    m = 8 * int(rng.integers(1, 97))
+    n = 8 * int(rng.integers(1, 97))
+    sk = int(rng.choice([2, 4, 8, 16]))
+    k = 8 * int(rng.integers(8 * sk, 8 * sk + 400))
+    out = t0g.BF16 if i % 2 else t0g.F32
+    _log(f"[case] fused sweep {i}: {layout} {m}x{n}x{k} {cfg.tile_m}x{cfg.tile_n} sk={sk} out={out}")
+    a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 300 + i)
+    da, db = rt.upload(a_st), rt.upload(b_st)
+    try:
+        name_f, fused = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_IN_KERNEL)
+        name_r, planes = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_REDUCE_KERNEL)
+        _log(f"[kernel] {name_f} / {name_r}")
+        assert np.array_equal(fused, planes), f"{name_f} differs from {name_r} + reduce kernel"
+        got = fused if out == t0g.F32 else o.bf16_to_f32(fused)
+        ok, relf, maxabs, bound = o.parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k)
+        assert ok if out == t0g.F32 else relf <= 5e-3, (relf, maxabs, bound)
     finally:
         rt.free(da)
         rt.free(db)
