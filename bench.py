@@ -82,6 +82,31 @@ def time_gemm(t0g, torch, rt, stream, m, n, k, layout, steps, warmup, seed=2, ou
     return res
 
 
+def c1_latency(t0g, torch, rt, stream, steps, warmup):
+    """256^3 NT, the reference's plumbing config: device time per launch (HIP events
+    around back-to-back launches), host time per asynchronous t0g_gemm call and per
+    call followed by t0g_wait_idle, both through this Python ctypes binding (the
+    reference quotes ~2.3 us per asynchronous and ~15 us per synchronous dispatch,
+    README.md:34, from Rust)."""
+    r = time_gemm(t0g, torch, rt, stream, 256, 256, 256, "NT", steps, warmup, seed=11)
+    desc = r["desc"]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rt.gemm_desc(desc)
+    t_async = (time.perf_counter() - t0) / steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rt.gemm_desc(desc)
+        rt.wait_idle()
+    t_sync = (time.perf_counter() - t0) / steps
+    sec = r["event_ms_per_launch"] * 1e-3
+    return {"device_us_per_launch": round(sec * 1e6, 2), "tflops": round(r["flop"] / sec / 1e12, 2),
+            "host_us_per_async_call": round(t_async * 1e6, 2), "host_us_per_sync_call": round(t_sync * 1e6, 2),
+            "kernel": r["kernel"], "host_path": "Python ctypes -> t0g_gemm"}
+
+
 MLP_SHAPES = [("NN", 1024, 11008, 4096), ("NN", 1024, 4096, 11008), ("NT", 1024, 11008, 4096),
               ("NT", 1024, 4096, 11008), ("TN", 11008, 4096, 1024), ("TN", 4096, 11008, 1024)]
 
@@ -610,6 +635,8 @@ def main():
                            "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1),
                            "frac_of_hbm": round(r["bytes_min"] / sec / 1e9 / PEAK_GBS, 4),
                            "us_per_gemm": round(sec * 1e6, 2), "kernel": r["kernel"]}
+        log("[bench] 256^3 NT (launch-latency config)")
+        extra["c1_256^3"] = c1_latency(t0g, torch, rt, stream, max(100, args.steps), max(20, args.warmup // 4))
         log("[bench] 4096^3 NN bf16 with fused bias + SiLU epilogue")
         rf = time_gemm(t0g, torch, rt, stream, M, N, K, "NN", args.steps, args.warmup // 2, epilogue_ops=["bias", "silu"])
         tf = rf["flop"] / (rf["event_ms_per_launch"] * 1e-3) / 1e12

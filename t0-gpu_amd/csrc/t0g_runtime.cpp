@@ -187,6 +187,10 @@ static int check_stream_k(t0g_device *dev) {
 
 // Wait for the stream with a time limit (the reference polls the AQL read
 // pointer for 5 s, src/kfd/mod.rs:1607-1642).  Timeout poisons the device.
+// The first 200 us poll without sleeping, as the reference does: a sleep of
+// the kernel's timer granularity (~60 us with the default timer slack) would
+// otherwise dominate a short GEMM's synchronous call.  Longer waits sleep
+// 20 us between polls.
 static int wait_stream(t0g_device *dev) {
     const double t0 = now_ms();
     const uint32_t limit = g_wait_timeout_ms.load();
@@ -194,10 +198,13 @@ static int wait_stream(t0g_device *dev) {
         hipError_t e = T0G_HIP(hipStreamQuery(dev->stream));
         if (e == hipSuccess) return check_stream_k(dev);
         if (e != hipErrorNotReady) return poison(dev, hip_fail(e, "hipStreamQuery"));
-        if (now_ms() - t0 > limit)
+        const double waited = now_ms() - t0;
+        if (waited > limit)
             return poison(dev, fail(T0G_ERR_TIMEOUT, "GPU wait timed out after %u ms", limit));
-        timespec ts = {0, 20000};
-        nanosleep(&ts, nullptr);
+        if (waited > 0.2) {
+            timespec ts = {0, 20000};
+            nanosleep(&ts, nullptr);
+        }
     }
 }
 
