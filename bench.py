@@ -494,7 +494,8 @@ def main():
                     help="time just this GEMM (bf16 out) and print its own JSON line; for profiling runs. "
                          "COPY:MiB instead times a plain device-to-device copy of that size, the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters; MLP or "
-                         "MLP_GROUPED times benchmark config 5's step (six GEMMs)")
+                         "MLP_GROUPED times benchmark config 5's step (six GEMMs); TORCH:LAYOUT:M:N:K "
+                         "times torch.mm (hipBLASLt) on the same inputs, for comparison runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures the GEMM on one GPU only "
@@ -541,6 +542,23 @@ def main():
         print(json.dumps({"only": args.only, "kernel": "t0g_f32_to_bf16_rne", "elements": n_el,
                           "us_per_launch": round(ms * 1e3, 2), "gbs": round(6.0 * n_el / (ms * 1e-3) / 1e9, 1)}),
               flush=True)
+        rt.set_stream(None)
+        rt.close()
+        return
+
+    if args.only and args.only.upper().startswith("TORCH:"):
+        lay, m, n, k = args.only.split(":")[1:5]
+        lay, m, n, k = lay.upper(), int(m), int(n), int(k)
+        if lay not in ("NN", "NT"):
+            raise SystemExit("TORCH: NN or NT only")
+        a, b = make_inputs(torch, m, n, k, lay, 2)
+        bb = b.t() if lay == "NT" else b   # 2-D mm with a transposed view: hipBLASLt's transB
+        c = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        ms = _event_ms(torch, stream, lambda: torch.mm(a, bb, out=c), args.steps, args.warmup)
+        flop = 2.0 * m * n * k
+        print(json.dumps({"only": args.only, "library": "torch.mm (hipBLASLt)", "us_per_launch": round(ms * 1e3, 2),
+                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                          "frac_of_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 4)}), flush=True)
         rt.set_stream(None)
         rt.close()
         return
