@@ -1338,16 +1338,11 @@ extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvert
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, f32, false)     \
     T0G_GEMM_LAYOUTS_D(PFX, BM, BN, WM, WN, bf16, true)
 
-// 256x256: 8 waves in ping-pong when A is K-contiguous (NN, NT), else the
-// 4-wave kernel (TN, TT: both operands are read with transposing LDS loads,
-// and 8 waves would read half as many fragments again per CU).
+// 256x256: the 4-wave kernel (one wave of 128x128 per SIMD) for every layout.
 #define T0G_GEMM_256(NAME, AK, BKM, OBF)                                                                  \
-    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
-        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmArgs p) {                \
-        if constexpr (AK)                                                                                 \
-            t0g::gemm_tile_pp<AK, BKM, OBF>(p);                                                          \
-        else                                                                                              \
-            t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                                      \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))         \
+        NAME(T0gGemmArgs p) {                                                                             \
+        t0g::gemm_tile_fast16<AK, BKM, OBF>(p);                                                          \
     }
 #define T0G_GEMM_LAYOUTS_256(OUTN, OBF)                                 \
     T0G_GEMM_256(t0g_gemm_256x256_k64_nt_##OUTN, true, true, OBF)       \
@@ -1361,12 +1356,9 @@ T0G_GEMM_LAYOUTS_256(bf16, true)
 // descriptors rebased per tile (K-contiguous operands) or per K stage
 // (M/N-contiguous), 64-bit byte counts.
 #define T0G_GEMM_256_X(NAME, AK, BKM, OBF)                                                                \
-    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
-        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmArgs p) {                \
-        if constexpr (AK)                                                                                 \
-            t0g::gemm_tile_pp<AK, BKM, OBF, true>(p);                                                    \
-        else                                                                                              \
-            t0g::gemm_tile_fast16<AK, BKM, OBF, true>(p);                                                \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))         \
+        NAME(T0gGemmArgs p) {                                                                             \
+        t0g::gemm_tile_fast16<AK, BKM, OBF, true>(p);                                                    \
     }
 #define T0G_GEMM_LAYOUTS_256_X(OUTN, OBF)                                   \
     T0G_GEMM_256_X(t0g_gemm_256x256_k64_nt_##OUTN##_x, true, true, OBF)     \
@@ -1406,12 +1398,9 @@ T0G_GEMM_TILE(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 T0G_GEMM_LAYOUTS_R(t0g_gemm_128x128_k64, 128, 128, 2, 2, f32, false)
 T0G_GEMM_LAYOUTS_R(t0g_gemm_128x128_k64, 128, 128, 2, 2, bf16, true)
 #define T0G_GEMM_256_R(NAME, AK, BKM, OBF)                                                                \
-    extern "C" __global__ void __launch_bounds__(AK ? 512 : 256)                                         \
-        __attribute__((amdgpu_waves_per_eu(AK ? 2 : 1, AK ? 2 : 1))) NAME(T0gGemmRedArgs ra) {            \
-        if constexpr (AK)                                                                                 \
-            t0g::gemm_tile_pp<AK, BKM, OBF, false, true>(ra.g, &ra);                                     \
-        else                                                                                              \
-            t0g::gemm_tile_fast16<AK, BKM, OBF, false, true>(ra.g, &ra);                                 \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))         \
+        NAME(T0gGemmRedArgs ra) {                                                                         \
+        t0g::gemm_tile_fast16<AK, BKM, OBF, false, true>(ra.g, &ra);                                     \
     }
 #define T0G_GEMM_LAYOUTS_256_R(OUTN, OBF)                                   \
     T0G_GEMM_256_R(t0g_gemm_256x256_k64_nt_##OUTN##_r, true, true, OBF)     \

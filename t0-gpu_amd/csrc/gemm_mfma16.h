@@ -108,9 +108,14 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
     // Fragment of 16-row sub-tile `sub` for 32-wide K step KK.
+    // The sub-tile offset is pointer arithmetic on an LDS pointer, so the
+    // compiler folds it into the instruction's offset field instead of adding
+    // it with VALU instructions.
     template <int KK>
     __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
-        return lds_load_b128(stage + frag[KK] + sub * 16 * kKRow);
+        const __attribute__((address_space(3))) bf16x8_t* base =
+            reinterpret_cast<const __attribute__((address_space(3))) bf16x8_t*>((uintptr_t)(stage + frag[KK]));
+        return base[sub * kKRow];   // sub * 16 rows of kKRow bytes, in 16-byte units
     }
 };
 
@@ -176,19 +181,21 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
-    // The stage base is a multiple of 1 KB, so (stage + frag0) ^ (sub << 5)
-    // addresses sub-tile `sub` of that stage.
+    // The stage base is a multiple of 1 KB and the XOR touches bits 5..8 only, so
+    // (stage + frag0) ^ (sub << 5) = stage + (frag0 ^ (sub << 5)) addresses
+    // sub-tile `sub` of that stage; the K step's row offsets are pointer
+    // arithmetic, folded into the instructions' offset fields.
     template <int KK>
     __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
         constexpr int O0 = KK * 32 * kRowB, O1 = (KK * 32 + 4) * kRowB;
-        const uint32_t a = (stage + frag0) ^ ((uint32_t)sub << 5);
-        short v[8];
-        short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
-        short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
-        lds_load_tr16(a + O0, lo);
-        lds_load_tr16(a + O1, hi);
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4s lds_v4s;
+        const __attribute__((address_space(3))) char* a = reinterpret_cast<const __attribute__((address_space(3))) char*>(
+            (uintptr_t)(stage + (frag0 ^ ((uint32_t)sub << 5))));
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(a + O0));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(a + O1));
         typedef short v8s __attribute__((ext_vector_type(8)));
-        const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+        const v8s w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return __builtin_bit_cast(bf16x8_t, w);
     }
 };
@@ -489,15 +496,28 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
     static_assert(SM % 2 == 0, "32-row staging blocks");
     const uint32_t l16 = lane & 15u, q = lane >> 4;
     const uint32_t rl = lane / kLanesPerRow, cl = (lane % kLanesPerRow) * kCols;
-    float bv[kCols];
+    // Without partials to add first (FIXUP), the chain runs on the accumulator
+    // layout before staging, 16 rows at a time on all of a lane's values (one
+    // bias value per sub-tile column); with them, after the sums, on the rows
+    // read back.  Bias reads past N return 0 (the descriptor's range).
+    float bv[kCols], bl[SN];
 #pragma unroll
     for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SN; ++j) bl[j] = 0.0f;
     if (p.flags & T0G_FLAG_BIAS) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)p.bias, 0, (int)(p.n * 4u), (int)kRsrcWord3);
+        if constexpr (FIXUP) {
 #pragma unroll
-        for (int c = 0; c < kCols; ++c)
-            bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + cl + c) * 4u, 0, 0));
+            for (int c = 0; c < kCols; ++c)
+                bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + cl + c) * 4u, 0, 0));
+        } else {
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+                bl[j] = __builtin_bit_cast(float,
+                                           __builtin_amdgcn_raw_buffer_load_b32(r, (col0 + j * 16 + l16) * 4u, 0, 0));
+        }
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     }
     const uint64_t cbase = p.c + (uint64_t)blockIdx.y * p.c_split_stride;
@@ -526,6 +546,23 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
 #pragma unroll
                     for (int j = 0; j < SN; ++j) x[ii][j] += t[ii][j];
             }
+        } else {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                float v[SN * 4], b4[SN * 4];
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        v[4 * j + r] = x[ii][j][r];
+                        b4[4 * j + r] = bl[j];
+                    }
+                apply_epilogue_n<SN * 4>(v, b4, epi_of(p));
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[ii][j][r] = v[4 * j + r];
+            }
         }
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii)
@@ -550,7 +587,7 @@ __device__ __forceinline__ void store_tile_vec16(const T0gGemmArgs& p, const f32
                 v[c + 2] = qv[2];
                 v[c + 3] = qv[3];
             }
-            apply_epilogue_n<kCols>(v, bv, epi_of(p));
+            if constexpr (FIXUP) apply_epilogue_n<kCols>(v, bv, epi_of(p));
             const uint32_t grow = row0 + i2 * 16 + rr, gcol = col0 + cl;
             const uint64_t addr = cbase + ((uint64_t)grow * p.ldc + gcol) * esize;
             if (vec) {
@@ -710,7 +747,7 @@ __device__ __forceinline__ void gemm_tile_fast16(const T0gGemmArgs& p, const T0g
 }
 
 
-// Ping-pong pipeline of the 8-wave 256x256 kernel.  Waves 0-3 (group 0) and
+// Ping-pong pipeline of the 8-wave stream-K 256x256 kernel (NN, NT).  Waves 0-3 (group 0) and
 // 4-7 (group 1) share the four SIMDs, one of each per SIMD, and alternate
 // between a load phase (fragment reads, DMA issue, waits) and a compute phase
 // (32 MFMAs and nothing else), offset by one phase: while one wave of a SIMD
@@ -781,75 +818,6 @@ __device__ __forceinline__ void k_pipeline_pp(f32x4_t (&acc)[SM][SN], const OpA&
         barrier_no_fence();
     }
     if (group == 0) barrier_no_fence();
-}
-
-// The 256x256 tile with 8 waves (2 x 4 of 128 x 64) in ping-pong: two waves per
-// SIMD, 128 accumulators each.  RED: split-K reduced inside the kernel.
-template <bool A_K, bool B_K, bool OUT_BF16, bool WIDE = false, bool RED = false>
-__device__ __forceinline__ void gemm_tile_pp(const T0gGemmArgs& p, const T0gGemmRedArgs* ra = nullptr) {
-    constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4;
-    constexpr int NT = 64 * WAVES_M * WAVES_N;
-    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
-    constexpr int SM = WTM / 16, SN = WTN / 16;
-    using OpA = Op16<A_K, BM, NT, SM, WIDE>;
-    using OpB = Op16<B_K, BN, NT, SN, WIDE>;
-    constexpr uint32_t A_BYTES = OpA::kStageBytes, STAGE = OpA::kStageBytes + OpB::kStageBytes;
-    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
-
-    tl_mark(p, 0);
-    const uint32_t tid = threadIdx.x;
-    uint32_t m0, n0;
-    tile_origin<BM, BN>(p, m0, n0);
-    const uint32_t kbeg = blockIdx.y * p.k_per_split;
-    const uint32_t kend = min(p.k, kbeg + p.k_per_split);
-    const int nst = kend > kbeg ? (int)((kend - kbeg + 63) / 64) : 0;
-    typename OpA::bytes_t a_bytes;
-    typename OpB::bytes_t b_bytes;
-    if constexpr (WIDE) {
-        a_bytes = operand_bytes_wide<A_K>(p.m, p.k, p.lda);
-        b_bytes = operand_bytes_wide<B_K>(p.n, p.k, p.ldb);
-    } else {
-        a_bytes = (A_K ? (p.m - 1) * p.lda + p.k : (p.k - 1) * p.lda + p.m) * 2;
-        b_bytes = (B_K ? (p.n - 1) * p.ldb + p.k : (p.k - 1) * p.ldb + p.n) * 2;
-    }
-
-    const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
-    OpA la;
-    OpB lb;
-    la.init(tid, m0, p.lda, wm * WTM);
-    lb.init(tid, n0, p.ldb, wn * WTN);
-
-    f32x4_t acc[SM][SN];
-#pragma unroll
-    for (int i = 0; i < SM; ++i)
-#pragma unroll
-        for (int j = 0; j < SN; ++j) acc[i][j] = f32x4_t{};
-
-    if (nst > 0) {
-        mfma16_drain();
-        const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-        const uint32_t group = wave >> 2;
-        if ((kend - kbeg) % 64 == 0)
-            k_pipeline_pp<false, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0, group);
-        else
-            k_pipeline_pp<true, A_BYTES, STAGE>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend, nst, lds0, group);
-    }
-
-    static_assert((NT / 64) * VecEpilogue16<SN>::kWaveBytes <= 2 * STAGE, "epilogue staging must fit the stages");
-    mfma16_drain();
-    T0G_WAIT_VMCNT(0);
-    barrier_no_fence();
-    tl_mark(p, 1);
-    if constexpr (RED) {
-        red_store_and_finish<BM, BN, NT, SM, SN, OUT_BF16>(p, *ra, acc, wm * WTM, wn * WTN, lane, wave, m0, n0,
-                                                           lds_addr(smem), 2 * STAGE);
-    } else {
-        const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
-        store_tile_vec16<SM, SN, OUT_BF16>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                           lds_addr(smem) + wave * VecEpilogue16<SN>::kWaveBytes, vec);
-    }
-    tl_mark(p, 2);
 }
 
 // ---- stream-K ------------------------------------------------------------------

@@ -37,7 +37,9 @@ int ok() {
 // the power-limited shader clock that data draws): time per wave of
 // workgroups = t0_us + (per-CU FLOP) / rate, linear in K to within a few
 // percent over K = 256 .. 8192.  64x64 gains throughput from co-resident
-// workgroups.  256x256 runs 8 waves (two per SIMD, in ping-pong).  Grids of at
+// workgroups.  256x256 runs 4 waves, one 128x128 wave tile per SIMD (its config
+// keeps wg_size 512, the unit of the reference-style thread grids; the
+// stream-K kernels for NN/NT run 8 waves in ping-pong).  Grids of at
 // most one workgroup per CU run the 64x64 and 128x128 deep-ring kernels, whose
 // fixed cost and rate were fitted on 256-workgroup grids over K = 512 .. 8192
 // (1024^2 and 2048^2 outputs); 128x128's two-workgroup rate on 4096^2 outputs.

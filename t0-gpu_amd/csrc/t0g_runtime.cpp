@@ -355,11 +355,10 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
                (uint64_t)sk * 256 <= (uint64_t)tile->bm * tile->bn &&
                red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
                red_grid * tile->bm * tile->bn * 4 < (1ull << 31);
-    // The 256x256 kernels with a K-contiguous A (NN, NT) run 8 waves in
-    // ping-pong; with an M-contiguous A (TN, TT) every fragment is a transposed
-    // LDS read and the 4-wave kernel, with half the fragment reads per CU, is
-    // faster.
-    p->wg = (tile->bm == 256 && !a_k_major(transpose)) ? 256u : tile->wg;
+    // The 256x256 kernels run 4 waves (one 128x128 wave tile per SIMD), except
+    // the stream-K ones with a K-contiguous A (NN, NT), which keep the 8-wave
+    // ping-pong schedule.
+    p->wg = (tile->bm == 256 && !(stream_k && a_k_major(transpose))) ? 256u : tile->wg;
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
                 ((out_bf16 && (!partial || p->fused)) ? "bf16" : "f32") +
                 (aligned ? (wide ? "_x" : deep ? (p->fused ? "_dr" : "_d") : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");

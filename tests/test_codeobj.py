@@ -45,13 +45,13 @@ def _gfx950_elf(blob):
 
 
 @pytest.mark.parametrize("symbol,args,lds,wg", [
-    ("t0g_gemm_256x256_k64_nt_f32", 104, 131072, 512),
+    ("t0g_gemm_256x256_k64_nt_f32", 104, 131072, 256),
     ("t0g_gemm_256x256_k64_tn_bf16", 104, 131072, 256),
     ("t0g_gemm_128x128_k64_nn_f32", 104, None, 256),
     ("t0g_gemm_64x64_k64_nt_f32_d", 104, None, 256),
     ("t0g_gemm_256x256_k64_nn_bf16_sk", 144, None, 512),
     ("t0g_gemm_256x256_k64_tt_f32_sk", 144, None, 256),
-    ("t0g_gemm_256x256_k64_nn_bf16_r", 144, None, 512),
+    ("t0g_gemm_256x256_k64_nn_bf16_r", 144, None, 256),
     ("t0g_gemm_128x128_k64_nt_f32_r", 144, None, 256),
     ("t0g_splitk_reduce_bf16", 80, 0, 256),
     ("t0g_f32_to_bf16_rne", 32, 0, 256),
@@ -140,8 +140,8 @@ def test_compile_returns_what_t0g_gemm_launches(blob):
     ck = t0g.gemm_compile(d)
     assert ck.name.decode() == t0g.gemm_kernel_name(d) == "t0g_gemm_256x256_k64_nn_bf16"
     assert ck.elf() == blob                       # the library's own code object
-    assert (ck.workgroup_size, ck.lds_size, ck.kernarg_size, ck.splits) == (512, 131072, 104, 1)
-    assert list(ck.grid) == [256 * 512, 1, 1]
+    assert (ck.workgroup_size, ck.lds_size, ck.kernarg_size, ck.splits) == (256, 131072, 104, 1)
+    assert list(ck.grid) == [256 * 256, 1, 1]
     f = _args(ck)
     assert (f["a"], f["b"], f["c"]) == (1 << 20, 1 << 26, 1 << 30)
     assert (f["m"], f["n"], f["k"], f["lda"], f["ldb"], f["ldc"]) == (4096,) * 6
