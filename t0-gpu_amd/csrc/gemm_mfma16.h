@@ -28,20 +28,6 @@ __device__ __forceinline__ uint32_t fm16(uint32_t k, uint32_t granules) {
     return (((0x7520u >> ((k & 3u) * 4)) & 0xFu) ^ ((k >> 3) & 1u)) & (granules - 1);
 }
 
-// DMA of one 16-byte piece per lane at voff + add: the add is done inside
-// the asm block so the per-instruction offsets are not kept in registers.
-__device__ __forceinline__ void dma16_add(u32x4_t rsrc, uint32_t voff, uint32_t add, uint32_t lds_m0) {
-    uint32_t tmp;
-    asm volatile(
-        "v_add_u32 %0, %1, %2\n\t"
-        "s_mov_b32 m0, %4\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %0, %3, 0 offen lds"
-        : "=&v"(tmp)
-        : "s"(add), "v"(voff), "s"(rsrc), "s"(lds_m0)
-        : "memory", "m0");
-}
-
 // WIDE: operands of any size (buffer descriptors rebased per tile or stage and
 // cut to 2 GiB, 64-bit byte counts); otherwise operands below 2^30 elements,
 // addressed from the operand base with 32-bit byte counts.
@@ -51,8 +37,9 @@ struct Op16;
 // K-contiguous operand of a 256-row tile, 64 K values per stage: 128-byte LDS
 // rows, chunk swizzle fk<64>.  DMA instruction i of a wave covers rows
 // 8 (i W + wave) + lane / 8 (W waves); for even W, fk<64> of those rows does not
-// depend on i, so one offset register and one K column serve all of a wave's
-// instructions.
+// depend on i, so one K column serves all of a wave's instructions, and their
+// byte offsets are kept in registers (the stage's K position is in the
+// descriptor's base).
 template <int ROWS, int NT, int SUBS, bool WIDE>
 struct Op16<true, ROWS, NT, SUBS, WIDE> {
     typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
@@ -67,6 +54,7 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
     uint32_t step;    // bytes between instructions (8 W rows)
     uint32_t wave;
     uint32_t frag[2];   // per 32-wide K step: LDS offset of the lane's chunk in sub-tile 0
+    uint32_t offs[kInstr];   // off0 + i * step: whole stages issue their DMA with no address arithmetic
 
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -82,6 +70,8 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
             off0 = ((row0 + r) * ld + c * 8) * 2;
         }
         step = 16 * kWaves * ld;
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) offs[i] = off0 + i * step;
         const uint32_t row = wrow + (lane & 15u), qk = lane >> 4;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) frag[kk] = row * kKRow + (((4u * kk + qk) ^ fk<64>(row)) << 4);
@@ -98,7 +88,7 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         if (CHECK)
             dma16(r, k0 + kcol < kend ? off0 + i * step : kOob, m0);
         else
-            dma16_add(r, off0, i * step, m0);
+            dma16(r, offs[i], m0);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
@@ -122,8 +112,8 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
 // M/N-contiguous operand of a 256-column tile: LDS rows are k rows of 512
 // bytes, granule swizzle fm16.  DMA instruction i of a wave covers k rows
 // 2 (i W + wave) + lane / 32 (W waves); their swizzle depends on i only through
-// bit 0 of i (W = 4) or not at all (W = 8), so two offset registers serve all
-// of a wave's instructions.
+// bit 0 of i (W = 4) or not at all (W = 8), so every instruction's byte offset
+// is one of two bases plus i steps, kept in registers.
 template <int ROWS, int NT, int SUBS, bool WIDE>
 struct Op16<false, ROWS, NT, SUBS, WIDE> {
     typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
@@ -139,6 +129,7 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
     uint32_t step;     // bytes between instructions (2 W k rows)
     uint32_t wave;
     uint32_t frag0;    // K step 0, half 0, sub-tile 0; sub-tile s is frag0 ^ (s << 5)
+    uint32_t offs[kInstr];   // off[i & 1] + i * step: whole stages issue their DMA with no address arithmetic
 
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -151,6 +142,8 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
             const uint32_t lg = (slot >> 1) ^ fm16(k + 2 * kWaves * i, kGranules);
             off[i] = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2;
         }
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) offs[i] = off[i & 1] + i * step;
         // ds_read_b64_tr_b16: 16-lane group q reads k rows 32*kk + 8q + 4h + r
         // (lane 4r + c: columns 4c .. 4c+3 of the 16-column sub-tile); lane i
         // of the group receives column i.  fm16 sees only k % 4 and bit 3 of k.
@@ -172,7 +165,7 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
         if (CHECK)
             dma16(r, k0 + krow + 2 * kWaves * i < kend ? off[i & 1] + i * step : kOob, m0);
         else
-            dma16_add(r, off[i & 1], i * step, m0);
+            dma16(r, offs[i], m0);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
