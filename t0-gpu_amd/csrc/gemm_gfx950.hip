@@ -647,6 +647,18 @@ __device__ __forceinline__ u32x4_t rsrc_words(uint64_t base, uint32_t bytes, uin
     return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
 }
 
+// rsrc_words for shifts below 2^32 (the operands of the non-wide kernels), in
+// 32-bit scalar arithmetic: the 64-bit compare of rsrc_words has no scalar
+// instruction and costs vector ones.  The words are uniform; readfirstlane
+// states it so they stay in scalar registers.
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+__device__ __forceinline__ u32x4_t rsrc_words32(uint64_t base, uint32_t bytes, uint32_t shift) {
+    const uint32_t rec = shift < bytes ? bytes - shift : 0u;
+    const uint64_t a = base + shift;
+    return u32x4_t{uniform_u32((uint32_t)a), uniform_u32((uint32_t)(a >> 32) & 0xFFFFu), uniform_u32(rec),
+                   (uint32_t)kRsrcWord3};
+}
+
 // Wide form of rsrc_words for operands of any size: [base + shift, base + bytes)
 // cut to its first 2 GiB (kOob stays out of range).  Callers shift it to the
 // tile's first row (K-contiguous operands) or the stage's first k row
@@ -678,6 +690,18 @@ __device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voff, uint32_t lds_
         :
         : "v"(voff), "s"(rsrc), "s"(lds_m0)
         : "memory", "m0");
+}
+
+// dma16 with the LDS address formed as lds_base + lds_off by one scalar add
+// straight into M0.
+__device__ __forceinline__ void dma16_at(u32x4_t rsrc, uint32_t voff, uint32_t lds_base, uint32_t lds_off) {
+    asm volatile(
+        "s_add_u32 m0, %2, %3\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %1, 0 offen lds"
+        :
+        : "v"(voff), "s"(rsrc), "s"(lds_base), "s"(lds_off)
+        : "memory", "m0", "scc");
 }
 
 // ---------------------------------------------------------------------------

@@ -80,7 +80,7 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         if constexpr (WIDE)
             return rsrc_words_wide(base + rowb, bytes > rowb ? bytes - rowb : 0u, (uint64_t)k0 * 2);
         else
-            return rsrc_words(base, bytes, (uint64_t)k0 * 2);
+            return rsrc_words32(base, bytes, k0 * 2);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
@@ -88,7 +88,7 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         if (CHECK)
             dma16(r, k0 + kcol < kend ? off0 + i * step : kOob, m0);
         else
-            dma16(r, offs[i], m0);
+            dma16_at(r, offs[i], lds + wave * 1024, i * kWaves * 1024);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
@@ -157,7 +157,7 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
         if constexpr (WIDE)
             return rsrc_words_wide(base, bytes, (uint64_t)k0 * ld * 2);
         else
-            return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+            return rsrc_words32(base, bytes, k0 * ld * 2);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
@@ -165,7 +165,7 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
         if (CHECK)
             dma16(r, k0 + krow + 2 * kWaves * i < kend ? off[i & 1] + i * step : kOob, m0);
         else
-            dma16(r, offs[i], m0);
+            dma16_at(r, offs[i], lds + wave * 1024, i * kWaves * 1024);
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
