@@ -47,11 +47,26 @@ int ok() {
 // its grid fetches twice the panel bytes of a 256x256 split-K grid, and inside
 // the MLP step (operands streamed from HBM) 1024x4096x11008 took 100-104 us
 // against 83 us alone: the rate below is the one measured in that setting.
+// 256x256 (4 waves): 4096x4096xK for K = 1024 .. 8192 gives 1.375 us per 64-K
+// stage per CU (6101 FLOP/ns) and 7.2 us per launch, with A and B resident in
+// the 256 MiB Infinity Cache; kRate256Hbm is the rate once they are not.
 const TileDef kTiles[kNumTiles] = {
-    {256, 256, 512, 1, 13.9, 5243.0, 5243.0, 0.0, 0.0, "t0g_gemm_256x256_k64"},
+    {256, 256, 512, 1, 7.2, 6101.0, 6101.0, 0.0, 0.0, "t0g_gemm_256x256_k64"},
     {128, 128, 256, 2, 4.75, 3628.0, 3628.0, 4.83, 3700.0, "t0g_gemm_128x128_k64"},
     {64, 64, 256, 4, 2.6, 931.0, 1606.0, 3.54, 2186.0, "t0g_gemm_64x64_k64"},
 };
+
+// 8192x11008x32768 (1.2 GB of operands, six rounds of 256 tiles) ran at 4952
+// FLOP/ns per CU.  Stream-K's 8-wave kernels run at 0.81 of the data-parallel
+// rate in either regime (4352x4096x8192: 267 us, 6144x11008x32768: 4327 us).
+constexpr double kRate256Hbm = 4952.0;
+constexpr double kInfinityCacheBytes = 256.0 * 1024 * 1024;
+constexpr double kStreamKRateFactor = 0.81;
+
+double rate256(uint32_t m, uint32_t k, uint32_t n) {
+    const double operands = 2.0 * ((double)m * k + (double)k * n);
+    return operands > kInfinityCacheBytes ? kRate256Hbm : kTiles[0].rate1;
+}
 
 const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size) {
     if (tile_k != kTileK) return nullptr;
@@ -123,11 +138,15 @@ double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint3
                             ? t.rate1 + (t.rate_full - t.rate1) * (resident - 1.0) / (double)(t.wg_per_cu - 1)
                             : t.rate1;
     const double flops_cu = per_cu * 2.0 * t.bm * t.bn * (kc > 0 ? kc : (double)kTileK);
-    double t_us = (deep ? t.t0_deep_us : waves * t.t0_us) + flops_cu / rate * 1e-3;
+    const double r = t.bm == 256 ? rate256(m, k, n) : rate;
+    double t_us = (deep ? t.t0_deep_us : waves * t.t0_us) + flops_cu / r * 1e-3;
     const double bytes = 2.0 * ((double)m * k + (double)k * n) + 2.0 * (double)m * n;
     const double t_mem = bytes / kPeakBytes * 1e6;
     if (t_mem > t_us) t_us = t_mem;
-    if (sk > 1) t_us += 2.5 + (double)sk * m * n * 4.0 / 4.5e6 + 0.25 * sk;
+    // The 256x256 kernels write their fp32 planes at about half the rate of the
+    // smaller tiles' (measured on split 8 and 16: 1024x2048x11008, 512x4096x11008,
+    // 256x4096x32768).
+    if (sk > 1) t_us += 2.5 + (double)sk * m * n * 4.0 / (t.bm == 256 ? 2.5e6 : 4.5e6) + 0.25 * sk;
     return t_us;
 }
 
@@ -143,7 +162,8 @@ double model_time_sk_us(uint32_t m, uint32_t k, uint32_t n) {
     if (total == 0) return 1e300;
     const uint64_t per_cu = (total + kNumCUs - 1) / kNumCUs;
     const bool cut = total % kNumCUs != 0 || per_cu % ipt != 0;
-    return t.t0_us + (double)per_cu * 2.0 * t.bm * t.bn * kTileK / t.rate1 * 1e-3 + (cut ? 30.0 : 5.0);
+    const double rate = kStreamKRateFactor * rate256(m, k, n);
+    return t.t0_us + (double)per_cu * 2.0 * t.bm * t.bn * kTileK / rate * 1e-3 + (cut ? 30.0 : 5.0);
 }
 
 void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, bool allow_stream_k) {
@@ -154,7 +174,11 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, boo
         for (uint32_t sk = 1; sk <= kMaxSplitK; sk *= 2) {
             if (sk > 1 && k < sk * 4 * kTileK) break;   // keep >= 4 K tiles per split
             const double tt = model_time_us(t, m, k, n, sk);
-            if (tt < best_t * 0.98) {   // prefer earlier (bigger tile, fewer splits) on near ties
+            // On a near tie keep the earlier choice (bigger tile, fewer splits),
+            // unless the later one needs fewer split planes: 128x128 split 4 took
+            // 68.6 us on 1024x1024x32768 against 83.2 us for 256x256 split 16,
+            // both modelled at 84.5 us.
+            if (tt < best_t * 0.98 || (tt <= best_t * 1.02 && sk < best_sk)) {
                 best_t = tt;
                 best = &t;
                 best_sk = sk;
@@ -162,16 +186,18 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, boo
         }
     }
     // Stream-K only where data-parallel rounds quantise badly: a last round at
-    // most an eighth full after at least one full one, and a clear modelled
-    // margin.  A part-empty round costs far less than its share of CUs
-    // suggests (the busy CUs clock up under the board power limit), so
-    // stream-K measured slower or equal at 144, 172 and 576 tiles and faster at
-    // 272 (4352x4096x8192: 267 us against 316 us); the tuner measures the rest.
+    // most an eighth full after at least one full one, and a modelled margin.
+    // A part-empty round costs far less than its share of CUs suggests (the
+    // busy CUs clock up under the board power limit), so stream-K measured
+    // slower or equal at 144, 172, 576 and 1032 tiles (6144x11008x4096: 472 us
+    // against 429 us) and faster at 258, 272 and 516 (4352x4096x8192: 230 us
+    // against 309 us; 3072x11008x4096: 231 us against 252 us); the tuner
+    // measures the rest.
     const TileDef &big = kTiles[0];
     const uint64_t tiles256 = (uint64_t)((m + big.bm - 1) / big.bm) * ((n + big.bn - 1) / big.bn);
     const uint64_t last_round = tiles256 % kNumCUs;
     if (allow_stream_k && tiles256 > kNumCUs && last_round != 0 && last_round * 8 <= kNumCUs &&
-        model_time_sk_us(m, k, n) < 0.85 * best_t) {
+        model_time_sk_us(m, k, n) < 0.95 * best_t) {
         best = &kTiles[0];
         best_sk = T0G_STREAM_K;
     }

@@ -100,11 +100,15 @@ def test_stream_k_plan(layout):
 
 
 @pytest.mark.parametrize("m,n,k,sk", [
-    # tile counts just past a multiple of 256: data-parallel needs a nearly empty last
-    # round (measured on MI355X: 4352x4096x8192, 272 tiles, 267 us stream-K vs 316 us)
-    (4352, 4096, 8192, True), (4352, 4096, 4096, True), (8448, 8192, 8192, True),
-    # fuller last rounds stay data-parallel (measured: 144 tiles a tie, 576 tiles slower)
-    (4608, 4608, 8192, False), (3072, 3072, 8192, False), (6144, 6144, 6144, False),
+    # tile counts just past one or two rounds of 256: data-parallel needs a nearly empty
+    # last round (measured on MI355X: 4352x4096x8192, 272 tiles, 230 us stream-K vs 309 us;
+    # 3072x11008x4096, 516 tiles, 231 vs 252 us; 1536x11008x32768, 258 tiles, 902 vs 1009 us
+    # for split 4)
+    (4352, 4096, 8192, True), (4352, 4096, 4096, True), (3072, 11008, 4096, True), (1536, 11008, 32768, True),
+    # fuller last rounds, or a thin last round after four full ones, stay data-parallel
+    # (measured: 144 tiles a tie, 576 tiles slower, 1032 tiles 472 vs 429 us)
+    (4608, 4608, 8192, False), (3072, 3072, 8192, False), (6144, 6144, 6144, False), (6144, 11008, 4096, False),
+    (8448, 8192, 8192, False),
     # The benchmark shapes keep their schedules (measured slower with stream-K: MLP 97 vs 88 us)
     (4096, 4096, 4096, False), (8192, 8192, 8192, False), (128, 4096, 4096, False), (256, 256, 32768, False),
     (1024, 11008, 4096, False), (1024, 4096, 11008, False), (11008, 4096, 1024, False), (256, 256, 256, False)])
