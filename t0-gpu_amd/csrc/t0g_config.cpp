@@ -57,7 +57,7 @@ const TileDef kTiles[kNumTiles] = {
 };
 
 // 8192x11008x32768 (1.2 GB of operands, six rounds of 256 tiles) ran at 4952
-// FLOP/ns per CU.  Stream-K's 8-wave kernels run at 0.81 of the data-parallel
+// FLOP/ns per CU.  The stream-K kernels run at 0.81 of the data-parallel
 // rate in either regime (4352x4096x8192: 267 us, 6144x11008x32768: 4327 us).
 constexpr double kRate256Hbm = 4952.0;
 constexpr double kInfinityCacheBytes = 256.0 * 1024 * 1024;
