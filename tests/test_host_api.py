@@ -29,6 +29,24 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_rust_binding_declares_every_entry_point():
+    """INTEGRATION.md's extern "C" block declares each function of the header with
+    the header's parameter count (the binding a Rust caller would paste)."""
+    with open(os.path.join(ROOT, "include", "t0g.h")) as f:
+        header = f.read()
+    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+        doc = f.read()
+
+    def nargs(a):
+        a = " ".join(a.split())
+        return 0 if a in ("", "void") else a.count(",") + 1
+
+    c_fns = {n: nargs(a) for n, a in re.findall(r"T0G_API\s+[^;(]*?\b(t0g_\w+)\s*\(([^;]*?)\);", header, re.S)}
+    rust_fns = {n: nargs(a) for n, a in re.findall(r"pub fn (t0g_\w+)\(([^;]*?)\)\s*(?:->[^;]*)?;", doc, re.S)}
+    assert sorted(set(c_fns) - set(rust_fns)) == []
+    assert {n: (rust_fns[n], c_fns[n]) for n in c_fns if rust_fns[n] != c_fns[n]} == {}
+
+
 def test_library_links_no_oracle():
     with open(t0g.LIB_PATH, "rb") as f:
         blob = f.read()
