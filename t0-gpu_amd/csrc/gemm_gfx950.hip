@@ -1056,6 +1056,124 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
 #undef T0G_KD
 }
 
+// Deep-ring K loop of the 64x64 tile (BK 64, one workgroup per CU, one 32x32
+// MFMA block per wave): the fragments of a whole stage are read one stage
+// ahead, right after the barrier that makes the stage visible, into one of
+// two register sets, so every LDS read has a stage of MFMAs, DMA issue and
+// the barrier to land.  Reading one K step ahead, as k_pipeline does, leaves
+// the wave's single MFMA per step waiting on that step's reads: C4a's
+// 128x4096x4096 (64x64, split 2) went from 15.2 to 14.1 us per call, C4b's
+// 256x256x32768 (split 16) from 15.3 to 13.7 us.  The 128x128 deep kernels
+// (four MFMA blocks per wave) keep k_pipeline: on this loop they ran 84 ->
+// 92 us on 1024x4096x11008.  MFMAs run in the same K order as k_pipeline's,
+// so the results are the same bit for bit.
+template <int KK, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void read_step(const OpA& la, const OpB& lb, uint32_t stage, bf16x8_t (&fa)[SM],
+                                          bf16x8_t (&fb)[SN]) {
+#pragma unroll
+    for (int i = 0; i < SM; ++i) fa[i] = la.template read_one<KK>(stage, i);
+#pragma unroll
+    for (int j = 0; j < SN; ++j) fb[j] = lb.template read_one<KK>(stage + OpA::kStageBytes, j);
+}
+
+template <int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void read_stage4(const OpA& la, const OpB& lb, uint32_t stage, bf16x8_t (&fa)[4][SM],
+                                            bf16x8_t (&fb)[4][SN]) {
+    read_step<0>(la, lb, stage, fa[0], fb[0]);
+    read_step<1>(la, lb, stage, fa[1], fb[1]);
+    read_step<2>(la, lb, stage, fa[2], fb[2]);
+    read_step<3>(la, lb, stage, fa[3], fb[3]);
+}
+
+// One K step's MFMAs with DMA instructions [DFIRST, DFIRST + DCOUNT) of the
+// stage being filled spread behind them.
+template <int DFIRST, int DCOUNT, bool CHECK, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void mfma_step_dma(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[SM],
+                                              const bf16x8_t (&fb)[SN], const OpA& la, const OpB& lb, uint32_t fill,
+                                              u32x4_t ra, u32x4_t rb, uint32_t kf, uint32_t kend) {
+    constexpr int kSlots = SM * SN;
+    constexpr int kPer = (DCOUNT + kSlots - 1) / kSlots;
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int q = DFIRST + (i * SN + j) * kPer + u;
+                if (q < DFIRST + DCOUNT) {
+                    if (q < OpA::kInstr)
+                        la.template issue_one<CHECK>(q, ra, fill, kf, kend);
+                    else
+                        lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + OpA::kStageBytes, kf, kend);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
+// One stage: read stage `nxt` into (na, nb), multiply the current stage from
+// (fa, fb), refill `fill` with stage kf's DMA, then wait for the stage two
+// ahead and meet at the barrier.
+template <bool CHECK, int NS, uint32_t STAGE, int kVmemPerStage, int SM, int SN, class OpA, class OpB>
+__device__ __forceinline__ void deep_stage(f32x16_t (&acc)[SM][SN], const bf16x8_t (&fa)[4][SM],
+                                           const bf16x8_t (&fb)[4][SN], bf16x8_t (&na)[4][SM], bf16x8_t (&nb)[4][SN],
+                                           const OpA& la, const OpB& lb, const T0gGemmArgs& p, uint32_t a_bytes,
+                                           uint32_t b_bytes, uint32_t nxt, uint32_t fill, uint32_t kf, uint32_t kend) {
+    constexpr int kPer = (kVmemPerStage + 3) / 4;
+#define T0G_KD4(i) ((i) * kPer < kVmemPerStage ? (i) * kPer : kVmemPerStage)
+    read_stage4(la, lb, nxt, na, nb);
+    const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+    const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+    mfma_step_dma<T0G_KD4(0), T0G_KD4(1) - T0G_KD4(0), CHECK>(acc, fa[0], fb[0], la, lb, fill, ra, rb, kf, kend);
+    mfma_step_dma<T0G_KD4(1), T0G_KD4(2) - T0G_KD4(1), CHECK>(acc, fa[1], fb[1], la, lb, fill, ra, rb, kf, kend);
+    mfma_step_dma<T0G_KD4(2), T0G_KD4(3) - T0G_KD4(2), CHECK>(acc, fa[2], fb[2], la, lb, fill, ra, rb, kf, kend);
+    mfma_step_dma<T0G_KD4(3), T0G_KD4(4) - T0G_KD4(3), CHECK>(acc, fa[3], fb[3], la, lb, fill, ra, rb, kf, kend);
+#undef T0G_KD4
+    T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // the stage two ahead has landed
+    barrier_no_fence();
+}
+
+template <bool CHECK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, int SM, int SN, class OpA,
+          class OpB>
+__device__ __forceinline__ void k_pipeline_deep(f32x16_t (&acc)[SM][SN], const OpA& la, const OpB& lb,
+                                                const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes,
+                                                uint32_t kbeg, uint32_t kend, int nst, uint32_t lds0) {
+    static_assert(NS >= 4, "ring of at least 4 stages");
+    constexpr uint32_t BK = 64;
+    bf16x8_t fa0[4][SM], fb0[4][SN], fa1[4][SM], fb1[4][SN];
+    // Prologue: stages 0 .. NS-2 in flight; stages 0 and 1 must have landed.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        la.template issue<CHECK>(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * BK, kend);
+        lb.template issue<CHECK>(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * BK, kend);
+    }
+    T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
+    barrier_no_fence();
+    read_stage4(la, lb, lds0, fa0, fb0);
+
+    uint32_t cur = 0;                  // byte offset of stage s's buffer
+    uint32_t fill = (NS - 1) * STAGE;  // buffer receiving stage s + NS - 1
+    for (int s = 0; s < nst; s += 2) {
+        {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            const uint32_t kf = kbeg + (uint32_t)(s + NS - 1) * BK;
+            deep_stage<CHECK, NS, STAGE, kVmemPerStage>(acc, fa0, fb0, fa1, fb1, la, lb, p, a_bytes, b_bytes,
+                                                        lds0 + nxt, lds0 + fill, kf, kend);
+            fill = cur;
+            cur = nxt;
+        }
+        if (s + 1 < nst) {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            const uint32_t kf = kbeg + (uint32_t)(s + NS) * BK;
+            deep_stage<CHECK, NS, STAGE, kVmemPerStage>(acc, fa1, fb1, fa0, fb0, la, lb, p, a_bytes, b_bytes,
+                                                        lds0 + nxt, lds0 + fill, kf, kend);
+            fill = cur;
+            cur = nxt;
+        }
+    }
+}
+
 }  // namespace t0g
 
 #include "gemm_red.h"
@@ -1118,12 +1236,21 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
         const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
         // Stages past a K tail need masked DMA; whole stages (the usual case)
         // skip the per-lane bound test.
-        if ((kend - kbeg) % BK == 0)
-            k_pipeline<false, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
-                                                                      nst, lds0);
-        else
-            k_pipeline<true, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg, kend,
-                                                                     nst, lds0);
+        if constexpr (BK == 64 && SM * SN == 1) {
+            if ((kend - kbeg) % BK == 0)
+                k_pipeline_deep<false, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg,
+                                                                          kend, nst, lds0);
+            else
+                k_pipeline_deep<true, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg,
+                                                                         kend, nst, lds0);
+        } else {
+            if ((kend - kbeg) % BK == 0)
+                k_pipeline<false, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg,
+                                                                          kend, nst, lds0);
+            else
+                k_pipeline<true, BK, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg,
+                                                                         kend, nst, lds0);
+        }
     }
 
     // Epilogue through LDS: 16-byte row stores for tiles wholly inside an
