@@ -1061,8 +1061,8 @@ __device__ __forceinline__ void k_pipeline(f32x16_t (&acc)[SM][SN], const OpA& l
 // ahead, right after the barrier that makes the stage visible, into one of
 // two register sets, so every LDS read has a stage of MFMAs, DMA issue and
 // the barrier to land.  Reading one K step ahead, as k_pipeline does, leaves
-// the wave's single MFMA per step waiting on that step's reads: C4a's
-// 128x4096x4096 (64x64, split 2) went from 15.2 to 14.1 us per call, C4b's
+// the wave's single MFMA per step waiting on that step's reads: the thin
+// 128x4096x4096 GEMM (64x64, split 2) went from 15.2 to 14.1 us per call,
 // 256x256x32768 (split 16) from 15.3 to 13.7 us.  The 128x128 deep kernels
 // (four MFMA blocks per wave) keep k_pipeline: on this loop they ran 84 ->
 // 92 us on 1024x4096x11008.  MFMAs run in the same K order as k_pipeline's,
