@@ -802,7 +802,7 @@ struct DmaOperand<true, ROWS, NT, SUBS, BK> {
         for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
     __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t, uint32_t k0) const {
-        return rsrc_words(base, bytes, (uint64_t)k0 * 2);
+        return rsrc_words32(base, bytes, k0 * 2u);
     }
     // CHECK: mask pieces at or past kend (a stage holding the K tail).  Without
     // it, pieces past kend read whatever follows in memory (or zero past the
@@ -810,7 +810,7 @@ struct DmaOperand<true, ROWS, NT, SUBS, BK> {
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
         const uint32_t voff = CHECK ? (k0 + kcol[i] < kend ? off[i] : kOob) : off[i];
-        dma16(r, voff, lds + (i * kWaves + wave) * 1024);
+        dma16_at(r, voff, lds, (i * kWaves + wave) * 1024);
     }
     // Fragment of sub-tile `sub` (32 rows x 8 K values) for K step KK of the
     // stage at LDS address `stage`.
@@ -871,7 +871,7 @@ struct DmaOperand<false, ROWS, NT, SUBS, BK> {
         for (int i = 0; i < kInstr; ++i) issue_one<CHECK>(i, r, lds, k0, kend);
     }
     __device__ __forceinline__ u32x4_t rsrc(uint64_t base, uint32_t bytes, uint32_t ld, uint32_t k0) const {
-        return rsrc_words(base, bytes, (uint64_t)k0 * ld * 2);
+        return rsrc_words32(base, bytes, k0 * ld * 2u);
     }
     // CHECK: mask pieces at or past kend (a stage holding the K tail).  Without
     // it, pieces past kend read whatever follows in memory (or zero past the
@@ -879,7 +879,7 @@ struct DmaOperand<false, ROWS, NT, SUBS, BK> {
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
         const uint32_t voff = CHECK ? (k0 + krow[i] < kend ? off[i] : kOob) : off[i];
-        dma16(r, voff, lds + (i * kWaves + wave) * 1024);
+        dma16_at(r, voff, lds, (i * kWaves + wave) * 1024);
     }
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
