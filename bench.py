@@ -246,7 +246,7 @@ def stream_k_extra(t0g, torch, rt, stream, steps, warmup):
     """The stream-K schedule against the data-parallel / split-K ones: a tile count
     just past 256 (272 tiles, where auto_select takes stream-K) and the MLP forward
     shape (172 tiles, where it does not)."""
-    p256 = t0g.GemmConfig.preset("tile_256x256_k64")
+    p256 = t0g.GemmConfig.preset("gfx950_256x256_k64")
     sk = p256.copy(split_k=t0g.STREAM_K)
     out = {}
     for lay, m, n, k, others in [("NN", 4352, 4096, 8192, {"dp": p256, "split2": p256.copy(split_k=2)}),

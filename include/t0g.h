@@ -77,17 +77,29 @@ typedef enum t0g_epilogue_op {
 
 typedef enum t0g_dtype { T0G_F32 = 0, T0G_BF16 = 1 } t0g_dtype;
 
-/* GemmConfig (src/t0/gemm_gen.rs:56-84).  Same fields and meaning; the valid
- * tile set is the MI355X one (t0g_config_preset).  split_k: 0 = None, or
- * T0G_STREAM_K. */
+/* GemmConfig (src/t0/gemm_gen.rs:56-84), also carrying a TileGemm
+ * (src/t0/tile_ir.rs:85-117; wg_size = TileGemm::wg_size() = tile_m).  Same
+ * fields and meaning.  Two kinds are valid:
+ *   - native: one of the gfx950 kernels exactly (t0g_config_preset "gfx950_*":
+ *     256x256 / 128x128 / 64x64, tile_k 64, wg_size 512 / 256 / 256, one pass);
+ *     it runs that kernel.
+ *   - reference space: every config gemm_gen::generate or lower_gemm takes
+ *     (the 14 GemmConfig and 17 TileGemm presets, tiles 16..256 in steps of 16,
+ *     tile_k 16..128, wave32 wg_size, 1..4 column passes).  Its grid in threads
+ *     and kernargs keep the reference's meaning (t0g_compute_grid*,
+ *     t0g_build_kernargs*); the runtime reads the problem from them and runs the
+ *     gfx950 tile the 256-CU model picks for it (an RDNA3 tile shape carries no
+ *     information about CDNA4).  Caller-owned split-K planes keep the
+ *     reference's K partition: plane s = K slice [s K/sk, (s+1) K/sk).
+ * split_k: 0 = None, or T0G_STREAM_K (native 256x256 only). */
 typedef struct t0g_gemm_config {
     uint32_t tile_m;
     uint32_t tile_n;
     uint32_t tile_k;
-    uint32_t wg_size;       /* threads per workgroup (wave64: 64 * waves) */
+    uint32_t wg_size;       /* threads per workgroup: the unit of the grid in threads */
     uint32_t split_k;       /* Option<u32>: 0 or 1 = no split */
     uint32_t lds_pad;       /* accepted for layout compatibility; the gfx950 kernels swizzle instead */
-    uint32_t n_col_passes;  /* must be 1 on gfx950 (one pass covers tile_n) */
+    uint32_t n_col_passes;  /* column passes: one workgroup's column block is tile_n * n_col_passes wide */
     uint8_t use_lds;
     uint8_t double_buffer;
     uint8_t swap_grid;      /* true: grid x -> N tiles, y -> M tiles (src/t0/gemm_gen.rs:286-296) */
@@ -114,11 +126,24 @@ T0G_API const char *t0g_version(void);
 
 /* ---- configuration and selection (host only, no GPU needed) ------------ */
 
-/* GemmConfig::tile_* presets (src/t0/gemm_gen.rs:88-145), MI355X tile set:
- * "tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64". */
+/* GemmConfig::tile_* presets (src/t0/gemm_gen.rs:88-145) by name, with the
+ * reference's field values ("tile_16x64_k16" ... "tile_64x128_2pass", 14 in
+ * all), plus the native configs "gfx950_256x256_k64", "gfx950_128x128_k64",
+ * "gfx950_64x64_k64". */
 T0G_API int t0g_config_preset(const char *name, t0g_gemm_config *out);
-/* generate()'s feasibility check (src/t0/gemm_gen.rs:253-266, is_feasible 194-197). */
+/* TileGemm::tile_* presets (src/t0/tile_ir.rs:121-358) by name, wg_size =
+ * tile_m as TileGemm::wg_size() gives it ("tile_128x64_k16" ...
+ * "tile_128x64_k64", 17 in all; the "_swap" ones without their acc_swap flag),
+ * plus the native "gfx950_*" configs. */
+T0G_API int t0g_tile_preset(const char *name, t0g_gemm_config *out);
+/* generate() / lower_gemm()'s acceptance (src/t0/gemm_gen.rs:253-266,
+ * src/t0/tile_ir.rs:624-655): native configs and the reference's config space
+ * (see t0g_gemm_config); RDNA3-only limits (its VGPR estimate) do not apply. */
 T0G_API int t0g_config_validate(const t0g_gemm_config *cfg);
+/* 1 if cfg names one gfx950 kernel exactly (it then runs that kernel), 0 for
+ * a reference-space config (it runs the tile the 256-CU model picks) or NULL.
+ * No reference counterpart. */
+T0G_API int t0g_config_is_native(const t0g_gemm_config *cfg);
 /* GemmConfig::n_waves (src/t0/gemm_gen.rs:152): wg_size / 64 on wave64. */
 T0G_API uint32_t t0g_config_n_waves(const t0g_gemm_config *cfg);
 /* GemmConfig::lds_total (src/t0/gemm_gen.rs:162-170). */

@@ -94,22 +94,37 @@ void make_config(const TileDef &t, uint32_t split_k, t0g_gemm_config *out) {
 
 uint32_t cfg_split(const t0g_gemm_config *cfg) { return cfg->split_k > 1 ? cfg->split_k : 1; }
 
+const TileDef *native_tile(const t0g_gemm_config *cfg) {
+    if (!cfg->use_lds || !cfg->double_buffer || cfg->n_col_passes != 1) return nullptr;
+    return find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
+}
+
+// The reference's config space: gemm_gen takes tile_m 16..128, tile_n 32..128,
+// tile_k 16/32/64, wave32 workgroups and 1-2 column passes
+// (src/t0/gemm_gen.rs:88-145, 684-803); tile_ir's TileGemm adds 256-row tiles,
+// tile_n in steps of 16 and tile_k 48/128 (src/t0/tile_ir.rs:85-358).  The
+// RDNA3 limits on top of that (VGPR estimate, LDS per WGP) do not apply here.
+static bool ref_shape(const t0g_gemm_config *cfg) {
+    auto step16 = [](uint32_t v, uint32_t hi) { return v >= 16 && v <= hi && v % 16 == 0; };
+    return step16(cfg->tile_m, 256) && step16(cfg->tile_n, 256) && step16(cfg->tile_k, 128) &&
+           cfg->wg_size >= 32 && cfg->wg_size <= 1024 && cfg->wg_size % 32 == 0 && cfg->n_col_passes >= 1 &&
+           cfg->n_col_passes <= 4;
+}
+
 int validate(const t0g_gemm_config *cfg) {
     if (!cfg) return fail(T0G_ERR_INVALID_ARG, "config is NULL");
-    if (!find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size))
+    if (!native_tile(cfg) && !ref_shape(cfg))
         return fail(T0G_ERR_UNSUPPORTED_CONFIG,
-                    "no gfx950 kernel for tile %ux%u k%u wg%u (supported: 256x256/128x128/64x64, k64, wg256)",
-                    cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
-    if (!cfg->use_lds || !cfg->double_buffer)
-        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "gfx950 kernels always use double-buffered LDS");
-    if (cfg->n_col_passes != 1)
-        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "n_col_passes must be 1 on gfx950 (got %u)", cfg->n_col_passes);
+                    "config %ux%u k%u wg%u passes %u is neither a gfx950 kernel (256x256/128x128/64x64 k64) nor in "
+                    "the reference's GemmConfig space (tiles 16..256 in steps of 16, tile_k 16..128, wg_size a "
+                    "multiple of 32, 1..4 column passes)",
+                    cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size, cfg->n_col_passes);
     if (cfg->transpose > T0G_TT) return fail(T0G_ERR_INVALID_ARG, "bad transpose %u", cfg->transpose);
     if (cfg->epilogue > T0G_EPI_BIAS_ADD_RELU) return fail(T0G_ERR_INVALID_ARG, "bad epilogue %u", cfg->epilogue);
     if (cfg->split_k == T0G_STREAM_K) {
-        if (cfg->tile_m != 256 || cfg->tile_n != 256)
-            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the 256x256 tile (got %ux%u)", cfg->tile_m,
-                        cfg->tile_n);
+        if (native_tile(cfg) != &kTiles[0])
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the gfx950 256x256 tile (got %ux%u wg%u)",
+                        cfg->tile_m, cfg->tile_n, cfg->wg_size);
         return ok();
     }
     const uint32_t sk = cfg_split(cfg);
@@ -204,6 +219,24 @@ void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, boo
     make_config(*best, best_sk, out);
 }
 
+// A native config runs its own kernel.  A config of the reference's space
+// (an RDNA3 tile, which says nothing about what is fast on 256 CDNA4 CUs) runs
+// on the gfx950 tile the model rates fastest for the problem at that split.
+const TileDef *plan_tile(const t0g_gemm_config *cfg, uint32_t m, uint32_t k, uint32_t n, uint32_t sk) {
+    if (const TileDef *t = native_tile(cfg)) return t;
+    if (sk == T0G_STREAM_K) return &kTiles[0];
+    const TileDef *best = &kTiles[0];
+    double best_t = 1e300;
+    for (const TileDef &t : kTiles) {
+        const double tt = model_time_us(t, m ? m : 1, k, n ? n : 1, sk ? sk : 1);
+        if (tt < best_t * 0.98) {
+            best_t = tt;
+            best = &t;
+        }
+    }
+    return best;
+}
+
 uint32_t legacy_chain(uint32_t epilogue) {
     if (epilogue == T0G_EPI_BIAS_ADD) return T0G_OP_BIAS_ADD;
     if (epilogue == T0G_EPI_BIAS_ADD_RELU) return T0G_OP_BIAS_ADD | (T0G_OP_RELU << 4);
@@ -245,18 +278,94 @@ extern "C" {
 const char *t0g_last_error(void) { return g_last_error.c_str(); }
 const char *t0g_version(void) { return "t0g 0.1.0 (gfx950)"; }
 
-int t0g_config_preset(const char *name, t0g_gemm_config *out) {
-    if (!name || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+namespace {
+struct RefPreset {
+    const char *name;
+    uint32_t tile_m, tile_n, tile_k, wg_size;
+    uint8_t use_lds, double_buffer, wgp_mode;
+    uint32_t n_col_passes;
+};
+
+// GemmConfig::tile_* (src/t0/gemm_gen.rs:88-145): field values as the
+// reference sets them (wave32 workgroups, WGP mode on, swap_grid on, NT,
+// no split, no padding).
+const RefPreset kGemmPresets[] = {
+    {"tile_16x64_k16", 16, 64, 16, 32, 1, 1, 1, 1},     {"tile_32x64_direct", 32, 64, 16, 64, 0, 0, 1, 1},
+    {"tile_32x64_k16", 32, 64, 16, 64, 1, 1, 1, 1},     {"tile_32x64_k32", 32, 64, 32, 64, 1, 1, 1, 1},
+    {"tile_32x128_k16", 32, 128, 16, 64, 1, 1, 1, 1},   {"tile_64x64_k16", 64, 64, 16, 64, 1, 1, 1, 1},
+    {"tile_64x64_k32", 64, 64, 32, 64, 1, 1, 1, 1},     {"tile_128x64_k16", 128, 64, 16, 128, 1, 1, 1, 1},
+    {"tile_64x128_k16", 64, 128, 16, 64, 1, 1, 1, 1},   {"tile_128x64_k32", 128, 64, 32, 128, 1, 1, 1, 1},
+    {"tile_128x128_k16", 128, 128, 16, 128, 1, 1, 1, 1}, {"tile_64x64_k64", 64, 64, 64, 64, 1, 1, 1, 1},
+    {"tile_128x128_2pass", 128, 64, 16, 128, 1, 1, 1, 2}, {"tile_64x128_2pass", 64, 64, 16, 64, 1, 1, 1, 2},
+};
+
+// TileGemm::tile_* (src/t0/tile_ir.rs:121-358): wg_size = tile_m (one wave32
+// per 32 rows, TileGemm::wg_size), double-buffered, no split.  acc_swap (the
+// _swap presets) is an RDNA3 register-pressure device with no field here.
+const RefPreset kTilePresets[] = {
+    {"tile_128x64_k16", 128, 64, 16, 128, 1, 1, 0, 1},       {"tile_64x64_k16", 64, 64, 16, 64, 1, 1, 0, 1},
+    {"tile_64x64_k32", 64, 64, 32, 64, 1, 1, 0, 1},          {"tile_64x64_k64", 64, 64, 64, 64, 1, 1, 0, 1},
+    {"tile_32x64_k16", 32, 64, 16, 32, 1, 1, 0, 1},          {"tile_128x64_k32", 128, 64, 32, 128, 1, 1, 0, 1},
+    {"tile_64x128_k32", 64, 128, 32, 64, 1, 1, 0, 1},        {"tile_64x128_k16", 64, 128, 16, 64, 1, 1, 0, 1},
+    {"tile_128x128_k16", 128, 128, 16, 128, 1, 1, 0, 1},     {"tile_128x128_k32", 128, 128, 32, 128, 1, 1, 1, 1},
+    {"tile_128x128_k48", 128, 128, 48, 128, 1, 1, 0, 1},     {"tile_128x128_k16_swap", 128, 128, 16, 128, 1, 1, 0, 1},
+    {"tile_128x128_k32_swap", 128, 128, 32, 128, 1, 1, 0, 1}, {"tile_256x64_k32_wgp", 256, 64, 32, 256, 1, 1, 1, 1},
+    {"tile_256x64_k64_wgp", 256, 64, 64, 256, 1, 1, 1, 1},   {"tile_128x128_k64", 128, 128, 64, 128, 1, 1, 0, 1},
+    {"tile_128x64_k64", 128, 64, 64, 128, 1, 1, 0, 1},
+};
+
+void from_preset(const RefPreset &p, t0g_gemm_config *out) {
+    memset(out, 0, sizeof *out);
+    out->tile_m = p.tile_m;
+    out->tile_n = p.tile_n;
+    out->tile_k = p.tile_k;
+    out->wg_size = p.wg_size;
+    out->use_lds = p.use_lds;
+    out->double_buffer = p.double_buffer;
+    out->wgp_mode = p.wgp_mode;
+    out->n_col_passes = p.n_col_passes;
+    out->swap_grid = 1;
+    out->transpose = T0G_NT;
+    out->epilogue = T0G_EPI_STORE_F32;
+}
+
+// The gfx950 kernels' own configs, named apart from the reference's presets.
+bool native_preset(const char *name, t0g_gemm_config *out) {
     for (const TileDef &t : kTiles) {
         char buf[64];
-        snprintf(buf, sizeof buf, "tile_%ux%u_k%u", t.bm, t.bn, kTileK);
+        snprintf(buf, sizeof buf, "gfx950_%ux%u_k%u", t.bm, t.bn, kTileK);
         if (strcmp(buf, name) == 0) {
             make_config(t, 0, out);
-            return ok();
+            return true;
         }
     }
+    return false;
+}
+}  // namespace
+
+int t0g_config_preset(const char *name, t0g_gemm_config *out) {
+    if (!name || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    for (const RefPreset &p : kGemmPresets)
+        if (strcmp(p.name, name) == 0) {
+            from_preset(p, out);
+            return ok();
+        }
+    if (native_preset(name, out)) return ok();
     return fail(T0G_ERR_UNSUPPORTED_CONFIG, "unknown preset '%s'", name);
 }
+
+int t0g_tile_preset(const char *name, t0g_gemm_config *out) {
+    if (!name || !out) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    for (const RefPreset &p : kTilePresets)
+        if (strcmp(p.name, name) == 0) {
+            from_preset(p, out);
+            return ok();
+        }
+    if (native_preset(name, out)) return ok();
+    return fail(T0G_ERR_UNSUPPORTED_CONFIG, "unknown TileGemm preset '%s'", name);
+}
+
+int t0g_config_is_native(const t0g_gemm_config *cfg) { return cfg && native_tile(cfg) ? 1 : 0; }
 
 int t0g_config_validate(const t0g_gemm_config *cfg) { return validate(cfg); }
 

@@ -46,7 +46,14 @@ int ok();
 const TileDef *find_tile(uint32_t tile_m, uint32_t tile_n, uint32_t tile_k, uint32_t wg_size);
 void make_config(const TileDef &t, uint32_t split_k, t0g_gemm_config *out);
 uint32_t cfg_split(const t0g_gemm_config *cfg);
+// Accepts a native config (exactly one of the gfx950 kernels) or any config of
+// the reference's GemmConfig / TileGemm space.
 int validate(const t0g_gemm_config *cfg);
+// The gfx950 tile of a native config (nullptr for a reference-space config).
+const TileDef *native_tile(const t0g_gemm_config *cfg);
+// The tile an m x n x k problem cut into sk K slices runs on under cfg: a
+// native config's own, else the modelled fastest (validated cfg).
+const TileDef *plan_tile(const t0g_gemm_config *cfg, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);
 // allow_stream_k = false: data-parallel configs only (the tile ABI launches).
 void select_config(uint32_t m, uint32_t k, uint32_t n, t0g_gemm_config *out, bool allow_stream_k = true);
 double model_time_us(const TileDef &t, uint32_t m, uint32_t k, uint32_t n, uint32_t sk);

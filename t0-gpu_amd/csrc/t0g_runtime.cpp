@@ -310,8 +310,13 @@ static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, 
 
 // allow_fused: the caller can run the in-kernel split-K reduction (its sync
 // words exist; not concurrent with another such launch of this device).
+// exact_split: K is cut into exactly split_req slices of k / split_req (the
+// caller guarantees the division and a multiple of 8 per slice: the fp32
+// planes are the caller's, with the reference's partition); otherwise slices
+// are rounded to whole 64-K stages and the split may shrink.
 static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, OperandPath path, uint32_t m,
-                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p, bool allow_fused = false) {
+                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p, bool allow_fused = false,
+                     bool exact_split = false) {
     const bool aligned = path != OperandPath::Elementwise, wide = path == OperandPath::Wide;
     bool stream_k = split_req == T0G_STREAM_K;
     if (stream_k) split_req = 1;
@@ -328,7 +333,9 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     p->tiles_n = (n + tile->bn - 1) / tile->bn;
     uint32_t sk = split_req ? split_req : 1;
     uint32_t kps = k;
-    if (sk > 1) {
+    if (exact_split && sk > 1) {
+        kps = k / sk;
+    } else if (sk > 1) {
         kps = ((k + sk - 1) / sk + kTileK - 1) / kTileK * kTileK;
         sk = (k + kps - 1) / kps;
         if (sk <= 1) {
@@ -581,11 +588,11 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
     cfg->epilogue = d->epi_chain ? (uint32_t)T0G_EPI_STORE_F32 : d->epilogue;
     if ((rc = validate(cfg))) return rc;
     const uint32_t sk = d->split_k ? d->split_k : cfg_split(cfg);
-    if (sk == T0G_STREAM_K && (cfg->tile_m != 256 || cfg->tile_n != 256))
-        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the 256x256 tile");
+    if (sk == T0G_STREAM_K && native_tile(cfg) != &kTiles[0])
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "stream-K needs the gfx950 256x256 tile");
     if (sk > kMaxSplitK && sk != T0G_STREAM_K)
         return fail(T0G_ERR_UNSUPPORTED_CONFIG, "split_k=%u > %u", sk, kMaxSplitK);
-    const TileDef *tile = find_tile(cfg->tile_m, cfg->tile_n, cfg->tile_k, cfg->wg_size);
+    const TileDef *tile = plan_tile(cfg, d->m, d->k, d->n, sk);
     const OperandPath path = operand_path(d->a, d->b, d->m, d->n, d->k, o->lda, o->ldb, t);
     if (path == OperandPath::Elementwise) {
         if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
@@ -1102,6 +1109,77 @@ static uint64_t rd_u64(const uint8_t *p) {
     return v;
 }
 
+static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d, bool allow_fused = true);
+
+// A reference-space config (an RDNA3 tile): the problem is the one the
+// reference's kernel for cfg computes from this grid and these kernargs, and
+// the gfx950 tile the model picks computes it.  The grid covers tiles_m row
+// blocks of tile_m and tiles_n column blocks of tile_n * n_col_passes
+// (compute_grid, src/t0/gemm_gen.rs:286-309); rows stop at M (tile_ir's
+// boundary masking, src/t0/tile_ir.rs:2374-2481; gemm_gen's M is the grid's)
+// and columns at N, which is also Y's row pitch.  o: the decoded kernargs
+// (m = M, n = N, ldc = N).
+static int dispatch_ref(t0g_device *dev, const t0g_kernel *kn, uint32_t tiles_m, uint32_t tiles_n, uint32_t sk,
+                        GemmOperands o, uint32_t y_split_stride) {
+    const t0g_gemm_config &cfg = kn->cfg;
+    const uint64_t rows = std::min<uint64_t>(o.m, (uint64_t)tiles_m * cfg.tile_m);
+    const uint64_t cols = std::min<uint64_t>(o.n, (uint64_t)tiles_n * cfg.tile_n * cfg.n_col_passes);
+    o.m = (uint32_t)rows;
+    o.n = (uint32_t)cols;
+    if (sk > 1 && y_split_stride != 0) {
+        // Caller-owned planes, summed by the caller in plane order
+        // (examples/test_gemm_correctness.rs:190-207): plane s at Y + s * y_split_stride
+        // holds K slice [s K/sk, (s+1) K/sk), as the reference's kernel cuts it
+        // (k_end = K >> split_k_shift, k_start = split id * k_end; src/t0/gemm_gen.rs:728-752).
+        if (o.k % (cfg.tile_k * sk) != 0)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG, "K=%u must be a multiple of tile_k*split_k=%u", o.k,
+                        cfg.tile_k * sk);
+        if (y_split_stride % 4 != 0)
+            return fail(T0G_ERR_INVALID_ARG, "y_split_stride=%u is not a whole number of f32", y_split_stride);
+        if (rows && cols && (uint64_t)y_split_stride / 4 < (rows - 1) * o.ldc + cols)
+            return fail(T0G_ERR_INVALID_ARG, "y_split_stride=%u bytes cannot hold a %llux%llu plane of pitch %u",
+                        y_split_stride, (unsigned long long)rows, (unsigned long long)cols, o.ldc);
+        if (o.chain != 0)
+            return fail(T0G_ERR_UNSUPPORTED_CONFIG,
+                        "an epilogue on caller-owned split-K planes would be applied to every partial sum; "
+                        "leave y_split_stride 0 (tile ABI) for a reduced, epilogued Y");
+        if (rows == 0 || cols == 0) return ok();
+        const TileDef *tile = plan_tile(&cfg, o.m, o.k, o.n, sk);
+        const OperandPath path = operand_path(o.a, o.b, o.m, o.n, o.k, o.lda, o.ldb, cfg.transpose);
+        int rc;
+        if (path == OperandPath::Elementwise) {
+            if ((rc = check_extent("X", o.m, o.lda))) return rc;
+            if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
+        }
+        GemmPlan p;
+        if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p, false, true))) return rc;
+        o.c_split_stride = y_split_stride;
+        return run_plan(dev, p, o, 0);
+    }
+    // One output (no split, or tile_ir's y_split_stride 0, whose planes the
+    // library keeps): the whole auto-selected plan, split and workspace included.
+    if (rows == 0 || cols == 0) return ok();
+    t0g_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = o.a;
+    d.b = o.b;
+    d.c = o.c;
+    d.bias = o.bias;
+    d.m = o.m;
+    d.n = o.n;
+    d.k = o.k;
+    d.lda = o.lda;
+    d.ldb = o.ldb;
+    d.ldc = o.ldc;
+    d.transpose = cfg.transpose;
+    d.out_dtype = T0G_F32;
+    d.epi_chain = o.chain;
+    d.epi_scale = o.epi_scale;
+    d.clamp_min = o.clamp_lo;
+    d.clamp_max = o.clamp_hi;
+    return gemm_locked(dev, &d);
+}
+
 // Interpret reference-layout kernargs + a thread grid for a GEMM kernel handle
 // and launch the equivalent gfx950 GEMM (see t0g_kernel_get / t0g_tile_kernel_get).
 static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t grid[3], const uint8_t *ka,
@@ -1151,6 +1229,7 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
     o.lda = o.k;
     o.ldb = cfg.transpose == T0G_NN ? o.n : o.k;
     o.ldc = o.n;
+    if (!native_tile(&cfg)) return dispatch_ref(dev, kn, tiles_m, tiles_n, sk, o, y_split_stride);
     // tile_ir split-K: build_kernargs_m always writes y_split_stride = 0 and
     // leaves the planes to the caller (src/t0/tile_ir.rs:3154-3157, 3179), so a
     // stride of 0 here means the library keeps the fp32 planes in its own
@@ -1335,7 +1414,7 @@ int t0g_gemm_compile(const t0g_gemm_desc *d, t0g_compiled_kernel *out) {
 
 // t0g_gemm with dev->mu held.  allow_fused = false: split-K with the separate
 // reduce kernel (launches that may overlap another on this device).
-static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d, bool allow_fused = true) {
+static int gemm_locked(t0g_device *dev, const t0g_gemm_desc *d, bool allow_fused) {
     t0g_gemm_config cfg;
     GemmPlan p;
     GemmOperands o;

@@ -295,7 +295,8 @@ bool load_entry(const t0g_tuner *t, const TuneKey &key, TuneEntry *e) {
     cfg.double_buffer = 1;
     cfg.transpose = key.transpose;
     cfg.epilogue = T0G_EPI_STORE_F32;
-    if (validate(&cfg)) return false;
+    // results of this build are gfx950 kernels; an RDNA3 tile here is not one of its files
+    if (validate(&cfg) || !native_tile(&cfg)) return false;
     if (key.kind == kTileIr && cfg.split_k == T0G_STREAM_K) return false;
     if (!read_ranking(js, &e->all)) e->all.clear();
     memset(&e->result, 0, sizeof e->result);
@@ -628,6 +629,8 @@ int t0g_tuner_store(t0g_tuner *tuner, const t0g_tune_result *result, const char 
     t0g_gemm_config cfg = result->best;
     cfg.transpose = key.transpose;
     if (int rc = validate(&cfg)) return rc;
+    if (!native_tile(&cfg))
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "a tuned config names a gfx950 kernel (t0g_config_is_native)");
     TuneEntry e;
     e.result = *result;
     e.result.best = cfg;
@@ -753,6 +756,8 @@ int t0g_tile_ir_store(t0g_tuner *tuner, const t0g_tune_result *result, const cha
     t0g_gemm_config cfg = result->best;
     cfg.transpose = T0G_NT;
     if (int rc = validate(&cfg)) return rc;
+    if (!native_tile(&cfg))
+        return fail(T0G_ERR_UNSUPPORTED_CONFIG, "a tuned config names a gfx950 kernel (t0g_config_is_native)");
     if (cfg.split_k == T0G_STREAM_K) return fail(T0G_ERR_UNSUPPORTED_CONFIG, "the tile ABI has no stream-K launch");
     TuneEntry e;
     e.result = *result;

@@ -76,9 +76,20 @@ class GemmConfig(ctypes.Structure):
 
     @staticmethod
     def preset(name):
+        """GemmConfig::tile_* (src/t0/gemm_gen.rs:88-145) or a native "gfx950_*" config."""
         cfg = GemmConfig()
         _check(_lib.t0g_config_preset(name.encode(), ctypes.byref(cfg)))
         return cfg
+
+    @staticmethod
+    def tile_preset(name):
+        """TileGemm::tile_* (src/t0/tile_ir.rs:121-358), wg_size = tile_m."""
+        cfg = GemmConfig()
+        _check(_lib.t0g_tile_preset(name.encode(), ctypes.byref(cfg)))
+        return cfg
+
+    def is_native(self):
+        return bool(_lib.t0g_config_is_native(ctypes.byref(self)))
 
     def copy(self, **changes):
         c = GemmConfig()
@@ -199,7 +210,9 @@ def _sig(name, restype, *argtypes):
 _sig("t0g_last_error", ctypes.c_char_p)
 _sig("t0g_version", ctypes.c_char_p)
 _sig("t0g_config_preset", ctypes.c_int, ctypes.c_char_p, _cfgp)
+_sig("t0g_tile_preset", ctypes.c_int, ctypes.c_char_p, _cfgp)
 _sig("t0g_config_validate", ctypes.c_int, _cfgp)
+_sig("t0g_config_is_native", ctypes.c_int, _cfgp)
 _sig("t0g_config_n_waves", _u32, _cfgp)
 _sig("t0g_config_lds_total", _u32, _cfgp)
 _sig("t0g_config_name", ctypes.c_int, _cfgp, ctypes.c_char_p, ctypes.c_size_t)

@@ -151,7 +151,7 @@ def test_compile_returns_what_t0g_gemm_launches(blob):
 
 
 def test_compile_split_k_writes_planes_to_c():
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=8)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(split_k=8)
     d = t0g.gemm_desc(1 << 20, 1 << 26, 1 << 30, 128, 4096, 4096, config=cfg)
     ck = t0g.gemm_compile(d)
     assert ck.splits == 8 and list(ck.grid) == [32 * 256, 8, 1]
@@ -163,7 +163,7 @@ def test_compile_split_k_writes_planes_to_c():
 
 
 def test_compile_stream_k_falls_back_to_the_same_tile():
-    cfg = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
     ck = t0g.gemm_compile(t0g.gemm_desc(1 << 20, 1 << 26, 1 << 30, 4352, 8192, 4096, transpose="NN", config=cfg))
     assert ck.name.decode() == "t0g_gemm_256x256_k64_nn_f32" and ck.splits == 1
 
@@ -197,7 +197,7 @@ def test_tile_auto_select_splits_the_hbm_bound_shapes():
 
 def test_tile_config_name_follows_tilegemm_name():
     """TileGemm::name's format (src/t0/tile_ir.rs:398-431): tile, k, _db, _skN, _mg, _wgp, _nn, epilogue."""
-    c = t0g.GemmConfig.preset("tile_128x128_k64")
+    c = t0g.GemmConfig.preset("gfx950_128x128_k64")
     assert t0g.tile_config_name(c) == "tile_gemm_128x128_k64_db"
     assert t0g.tile_config_name(c.copy(split_k=8)) == "tile_gemm_128x128_k64_db_sk8"
     assert t0g.tile_config_name(c.copy(transpose=t0g.NN, swap_grid=0)) == "tile_gemm_128x128_k64_db_mg_nn"

@@ -96,7 +96,7 @@ def check_parity(c_gpu, c_ref, k, label):
     assert ok, f"{label}: relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
 
 
-PRESETS = ["tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
+PRESETS = ["gfx950_256x256_k64", "gfx950_128x128_k64", "gfx950_64x64_k64"]
 
 
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
@@ -287,7 +287,7 @@ def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
     check_parity(host, o.gemm("NT", a_mk, b_nk, m, n, k), k, f"reduce order {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("preset", ["tile_64x64_k64", "tile_128x128_k64"])
+@pytest.mark.parametrize("preset", ["gfx950_64x64_k64", "gfx950_128x128_k64"])
 @pytest.mark.parametrize("tiles_m,tiles_n,sk,layout", [(1, 1, 8, "NT"), (2, 2, 2, "NN"), (1, 3, 8, "TN"),
                                                        (2, 3, 4, "NT"), (4, 4, 16, "NN"), (1, 5, 8, "NT"),
                                                        (3, 2, 4, "TT"), (2, 4, 3, "NT"), (1, 7, 3, "NN"),
@@ -350,7 +350,7 @@ def test_tile_remap_256_covers_every_tile(rt, bufs, tiles_m, tiles_n, layout):
     b = bufs.up(b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T))
     c = bufs.alloc(m * n * 4, fill=0xFF)
     d = t0g.gemm_desc(a, b, c, m, n, k, transpose=layout, out_dtype=t0g.F32,
-                      config=t0g.GemmConfig.preset("tile_256x256_k64"))
+                      config=t0g.GemmConfig.preset("gfx950_256x256_k64"))
     assert "256x256" in t0g.gemm_kernel_name(d)
     rt.gemm_desc(d)
     rt.wait_idle()
@@ -432,8 +432,8 @@ def test_c5_mlp_step(rt, bufs):
 
 # ---- the reference's own call sequence: select -> kernel -> kernargs -> grid -> dispatch ----
 
-REF_CFGS = [("tile_64x64_k64", 0), ("tile_128x128_k64", 0), ("tile_128x128_k64", 2), ("tile_64x64_k64", 4),
-            ("tile_64x64_k64", 8), ("tile_256x256_k64", 0)]
+REF_CFGS = [("gfx950_64x64_k64", 0), ("gfx950_128x128_k64", 0), ("gfx950_128x128_k64", 2), ("gfx950_64x64_k64", 4),
+            ("gfx950_64x64_k64", 8), ("gfx950_256x256_k64", 0)]
 REF_SIZES = [(64, 64, 64), (128, 128, 128), (256, 256, 256), (64, 256, 64), (128, 1024, 256), (256, 512, 512)]
 
 
@@ -470,7 +470,7 @@ def test_reference_dispatch_sequence(rt, bufs, preset, sk):
 def test_tile_dispatch_with_m_and_ragged_edges(rt, bufs):
     """tile_ir ABI (build_kernargs_m, src/t0/tile_ir.rs:3173) on M/N that are not
     tile multiples, NN layout (B stored [K][N])."""
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(transpose=t0g.NN)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(transpose=t0g.NN)
     kern = rt.ensure_tile_kernel(cfg)
     m, k, n = 200, 192, 136
     a = o.make_bf16_suite(m * k, 1).reshape(m, k)
@@ -560,7 +560,7 @@ def test_raw_kernel_load_and_dispatch(rt, bufs):
 
 
 def test_invalid_dispatch_is_rejected(rt, bufs):
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64").copy(split_k=4)
     kern = rt.ensure_gemm_kernel(cfg)
     ka = bytearray(t0g.build_kernargs(1 << 20, 1 << 21, 1 << 22, 512, 64, 64, cfg))
     ka[36:40] = b"\0\0\0\0"   # y_split_stride = 0 with split_k > 1
@@ -600,8 +600,8 @@ def test_injected_failure_poisons_the_device():
 # ---- fused epilogue chains (tile_ir EpilogueOp, src/t0/tile_ir.rs:41-62) ----
 CHAINS = [("relu",), ("silu",), ("gelu",), ("abs",), ("neg",), ("scale",), ("clamp",), ("bias", "relu"),
           ("bias", "scale", "silu"), ("gelu", "neg", "abs", "clamp")]
-CHAIN_CASES = [("tile_256x256_k64", "NN"), ("tile_256x256_k64", "TN"), ("tile_128x128_k64", "NT"),
-               ("tile_64x64_k64", "TT")]
+CHAIN_CASES = [("gfx950_256x256_k64", "NN"), ("gfx950_256x256_k64", "TN"), ("gfx950_128x128_k64", "NT"),
+               ("gfx950_64x64_k64", "TT")]
 
 
 def _chain_case(m, n, k, layout, seed):
@@ -659,7 +659,7 @@ def test_reference_epilogue_e2e_through_tile_abi(rt, bufs, op):
     own assertions (|err| <= 0.1 everywhere; ReLU zeroes every significant negative;
     Abs leaves nothing negative) plus the north-star gate."""
     m = k = n = 64
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64")
     chain = t0g.epilogue_chain([op])
     kern = rt.ensure_tile_kernel(cfg, epilogue_chain=chain)
     x, wt = _reference_epilogue_inputs(m, k, n)
@@ -682,7 +682,7 @@ def test_reference_epilogue_e2e_through_tile_abi(rt, bufs, op):
 def test_tile_abi_chain_with_all_arguments(rt, bufs):
     """Bias (at the unaligned offset 44), scale and clamp arguments read from the
     tile kernargs, on a ragged NN problem."""
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(transpose=t0g.NN)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(transpose=t0g.NN)
     ops = ["bias", "scale", "silu", "clamp"]
     chain = t0g.epilogue_chain(ops)
     kern = rt.ensure_tile_kernel(cfg, epilogue_chain=chain)
@@ -849,7 +849,7 @@ def test_gemm_group_equals_one_by_one(rt, bufs):
     enqueued as one group over the device stream and two side streams: every output
     equals the same GEMM run alone, bit for bit, twice in a row; then work on the
     device stream sees all of them finished."""
-    p256 = t0g.GemmConfig.preset("tile_256x256_k64")
+    p256 = t0g.GemmConfig.preset("gfx950_256x256_k64")
     sk = p256.copy(split_k=t0g.STREAM_K)
     cases = [  # (layout, m, n, k, out, extra desc fields, config used alone)
         ("NN", 1024, 4096, 11008, t0g.BF16, {}, None),                          # split 4 + reduce

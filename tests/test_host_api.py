@@ -56,13 +56,13 @@ def test_library_links_no_oracle():
 def test_version_and_last_error():
     assert "gfx950" in t0g.version()
     with pytest.raises(t0g.T0gError) as e:
-        t0g.GemmConfig.preset("tile_64x64_k16")   # an RDNA3 preset: no gfx950 kernel
+        t0g.GemmConfig.preset("tile_96x64_k16")   # no such preset in gemm_gen.rs:88-145
     assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG
     assert "unknown preset" in t0g.last_error()
 
 
-@pytest.mark.parametrize("name,bm,bn,wg", [("tile_256x256_k64", 256, 256, 512), ("tile_128x128_k64", 128, 128, 256),
-                                           ("tile_64x64_k64", 64, 64, 256)])
+@pytest.mark.parametrize("name,bm,bn,wg", [("gfx950_256x256_k64", 256, 256, 512), ("gfx950_128x128_k64", 128, 128, 256),
+                                           ("gfx950_64x64_k64", 64, 64, 256)])
 def test_presets_and_derived_fields(name, bm, bn, wg):
     c = t0g.GemmConfig.preset(name)
     c.validate()
@@ -78,12 +78,111 @@ def test_presets_and_derived_fields(name, bm, bn, wg):
 
 
 def test_invalid_configs_are_errors_not_panics():
-    c = t0g.GemmConfig.preset("tile_128x128_k64")
-    for bad in (dict(tile_m=96), dict(tile_k=16), dict(wg_size=128), dict(split_k=3), dict(split_k=128),
-                dict(n_col_passes=2), dict(double_buffer=0)):
+    c = t0g.GemmConfig.preset("gfx950_128x128_k64")
+    # outside both the native set and the reference's space (gemm_gen.rs:684-803 panics on these)
+    for bad in (dict(tile_m=8), dict(tile_m=24), dict(tile_m=272), dict(tile_n=8), dict(tile_k=8), dict(tile_k=24),
+                dict(tile_k=144), dict(wg_size=0), dict(wg_size=48), dict(wg_size=2048), dict(n_col_passes=0),
+                dict(n_col_passes=5), dict(split_k=3), dict(split_k=128)):
         with pytest.raises(t0g.T0gError) as e:
             c.copy(**bad).validate()
         assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG, bad
+    with pytest.raises(t0g.T0gError) as e:
+        c.copy(transpose=4).validate()
+    assert e.value.code == t0g.ERR_INVALID_ARG
+    # stream-K needs the native 256x256 kernel, not merely a 256x256 tile shape
+    with pytest.raises(t0g.T0gError):
+        t0g.GemmConfig.preset("gfx950_256x256_k64").copy(wg_size=256, split_k=t0g.STREAM_K).validate()
+    with pytest.raises(t0g.T0gError):
+        t0g.GemmConfig.preset("tile_64x64_k16").copy(split_k=t0g.STREAM_K).validate()
+
+
+def test_off_native_variants_are_reference_space_configs():
+    # what used to be refused (another tile_k, wg_size, pass count or no LDS) is now a config of
+    # the reference's space: valid, and run on the modelled tile rather than its own kernel
+    c = t0g.GemmConfig.preset("gfx950_128x128_k64")
+    assert c.is_native()
+    for var in (dict(tile_m=96), dict(tile_k=16), dict(wg_size=128), dict(n_col_passes=2), dict(double_buffer=0)):
+        v = c.copy(**var)
+        v.validate()
+        assert not v.is_native(), var
+
+
+# GemmConfig::tile_* (src/t0/gemm_gen.rs:88-145): (name, tile_m, tile_n, tile_k, wg_size, use_lds, passes)
+GEMM_PRESETS = [("tile_16x64_k16", 16, 64, 16, 32, 1, 1), ("tile_32x64_direct", 32, 64, 16, 64, 0, 1),
+                ("tile_32x64_k16", 32, 64, 16, 64, 1, 1), ("tile_32x64_k32", 32, 64, 32, 64, 1, 1),
+                ("tile_32x128_k16", 32, 128, 16, 64, 1, 1), ("tile_64x64_k16", 64, 64, 16, 64, 1, 1),
+                ("tile_64x64_k32", 64, 64, 32, 64, 1, 1), ("tile_128x64_k16", 128, 64, 16, 128, 1, 1),
+                ("tile_64x128_k16", 64, 128, 16, 64, 1, 1), ("tile_128x64_k32", 128, 64, 32, 128, 1, 1),
+                ("tile_128x128_k16", 128, 128, 16, 128, 1, 1), ("tile_64x64_k64", 64, 64, 64, 64, 1, 1),
+                ("tile_128x128_2pass", 128, 64, 16, 128, 1, 2), ("tile_64x128_2pass", 64, 64, 16, 64, 1, 2)]
+
+
+@pytest.mark.parametrize("name,bm,bn,bk,wg,lds,passes", GEMM_PRESETS)
+def test_reference_gemm_presets(name, bm, bn, bk, wg, lds, passes):
+    c = t0g.GemmConfig.preset(name)
+    c.validate()
+    assert not c.is_native()
+    assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size, c.use_lds, c.double_buffer, c.n_col_passes) == \
+        (bm, bn, bk, wg, lds, lds, passes)
+    assert (c.split_k, c.lds_pad, c.swap_grid, c.wgp_mode, c.transpose, c.epilogue) == (0, 0, 1, 1, t0g.NT, 0)
+    # GemmConfig::name (gemm_gen.rs:207-227): lds tag, pass tag, then _wgp
+    tag = "_ldsdb" if lds else "_direct"
+    ptag = f"_{passes}p" if passes > 1 else ""
+    assert c.name() == f"t0_gemm_{bm}x{bn}_k{bk}{tag}{ptag}_wgp"
+    assert c.copy(split_k=4).name() == f"t0_gemm_{bm}x{bn}_k{bk}{tag}_sk4{ptag}_wgp"
+    assert c.lds_total() == (bm + bn) * bk * 2 * (2 if lds else 1)   # lds_total (gemm_gen.rs:162-170)
+    # compute_grid (gemm_gen.rs:286-309): threads of the caller's wg_size, columns per pass block
+    tm, tn = -(-1000 // bm), -(-3000 // (bn * passes))
+    assert t0g.compute_grid(c, 1000, 3000) == (tn * wg, tm)
+    assert t0g.compute_grid_split_k(c, 1000, 3000, 4) == (tn * wg, tm * 4)
+    assert t0g.compute_grid(c.copy(swap_grid=0), 1000, 3000) == (tm * wg, tn)
+
+
+def test_reference_gemm_preset_count_and_sweep_list():
+    assert len(GEMM_PRESETS) == 14
+    # sweep_configs() (gemm_gen.rs:233-245) draws on these presets; all are valid configs here
+    for name in ("tile_16x64_k16", "tile_32x64_k16", "tile_32x64_k32", "tile_32x128_k16", "tile_64x64_k16",
+                 "tile_64x64_k32", "tile_128x64_k16", "tile_64x128_k16", "tile_128x64_k32"):
+        t0g.GemmConfig.preset(name).validate()
+
+
+# TileGemm::tile_* (src/t0/tile_ir.rs:121-358): (name, tile_m, tile_n, tile_k, wgp)
+TILE_PRESETS = [("tile_128x64_k16", 128, 64, 16, 0), ("tile_64x64_k16", 64, 64, 16, 0),
+                ("tile_64x64_k32", 64, 64, 32, 0), ("tile_64x64_k64", 64, 64, 64, 0),
+                ("tile_32x64_k16", 32, 64, 16, 0), ("tile_128x64_k32", 128, 64, 32, 0),
+                ("tile_64x128_k32", 64, 128, 32, 0), ("tile_64x128_k16", 64, 128, 16, 0),
+                ("tile_128x128_k16", 128, 128, 16, 0), ("tile_128x128_k32", 128, 128, 32, 1),
+                ("tile_128x128_k48", 128, 128, 48, 0), ("tile_128x128_k16_swap", 128, 128, 16, 0),
+                ("tile_128x128_k32_swap", 128, 128, 32, 0), ("tile_256x64_k32_wgp", 256, 64, 32, 1),
+                ("tile_256x64_k64_wgp", 256, 64, 64, 1), ("tile_128x128_k64", 128, 128, 64, 0),
+                ("tile_128x64_k64", 128, 64, 64, 0)]
+
+
+@pytest.mark.parametrize("name,bm,bn,bk,wgp", TILE_PRESETS)
+def test_reference_tile_presets(name, bm, bn, bk, wgp):
+    c = t0g.GemmConfig.tile_preset(name)
+    c.validate()
+    assert not c.is_native()
+    assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size, c.wgp_mode, c.double_buffer, c.split_k) == \
+        (bm, bn, bk, bm, wgp, 1, 0)                                   # TileGemm::wg_size() = tile_m
+    # tile_ir::compute_grid (tile_ir.rs:3193-3202)
+    assert t0g.tile_compute_grid(c, 129, 65) == [-(-65 // bn) * bm, -(-129 // bm), 1]
+    db_wgp = "_db" + ("_wgp" if wgp else "")
+    assert t0g.tile_config_name(c) == f"tile_gemm_{bm}x{bn}_k{bk}{db_wgp}"
+
+
+def test_reference_configs_run_on_the_modelled_native_tile():
+    # a reference config names an RDNA3 tile; the kernel is the gfx950 tile the 256-CU model picks
+    ref = t0g.GemmConfig.preset("tile_64x64_k16")
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, config=ref)
+    assert t0g.gemm_kernel_name(d) == "t0g_gemm_256x256_k64_nt_f32"
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, config=ref.copy(split_k=4))
+    assert t0g.gemm_kernel_name(d).startswith("t0g_gemm_256x256_k64_nt_f32")
+    assert t0g.gemm_workspace_size(d) == 4 * 4096 * 4096 * 4          # the config's split is kept
+    # a native config still runs its own kernel, whatever the model would pick
+    nat = t0g.GemmConfig.preset("gfx950_64x64_k64")
+    d = t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, config=nat)
+    assert t0g.gemm_kernel_name(d).startswith("t0g_gemm_64x64_k64_nt_f32")
 
 
 def test_auto_select_reference_assertions():
@@ -115,7 +214,7 @@ def test_auto_select_table_for_256_cus():
 
 
 def test_compute_grid_formulas():
-    c = t0g.GemmConfig.preset("tile_128x128_k64")
+    c = t0g.GemmConfig.preset("gfx950_128x128_k64")
     assert t0g.compute_grid(c, 1000, 300) == (3 * 256, 8)          # ceil(300/128)*wg, ceil(1000/128)
     assert t0g.compute_grid(c.copy(swap_grid=0), 1000, 300) == (8 * 256, 3)
     assert t0g.compute_grid_split_k(c, 256, 256, 4) == (2 * 256, 2 * 4)
@@ -127,7 +226,7 @@ def test_compute_grid_formulas():
 
 
 def test_build_kernargs_layout():
-    c = t0g.GemmConfig.preset("tile_64x64_k64")
+    c = t0g.GemmConfig.preset("gfx950_64x64_k64")
     ka = t0g.build_kernargs(0x1000, 0x2000, 0x3000, 64, 96, 128, c)
     assert len(ka) == 40
     assert struct.unpack("<QQQIIII", ka) == (0x1000, 0x2000, 0x3000, 64, 96, 0, 0)
@@ -181,8 +280,8 @@ def test_split_k_mode_selects_the_reduction():
     def name(m=128, n=4096, **kw):
         return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, m, n, 4096, transpose="NT",
                                                   out_dtype=t0g.BF16, **kw))
-    c128 = t0g.GemmConfig.preset("tile_128x128_k64")
-    c64 = t0g.GemmConfig.preset("tile_64x64_k64")
+    c128 = t0g.GemmConfig.preset("gfx950_128x128_k64")
+    c64 = t0g.GemmConfig.preset("gfx950_64x64_k64")
     # 32 tiles x 8 slices: one workgroup per CU, so the deep-ring kernel writes the planes
     assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
     t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
@@ -250,7 +349,7 @@ def test_epilogue_chain_packing_names_and_kernargs():
         t0g.epilogue_chain(["relu"] * 9)
     with pytest.raises(t0g.T0gError):
         t0g.epilogue_chain_name(0x30)                 # a gap before an op
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64")
     base = t0g.build_kernargs_m(1, 2, 3, 64, 32, 16, cfg)
     ka = t0g.build_kernargs_m_epilogue(1, 2, 3, 64, 32, 16, cfg, t0g.epilogue_chain(["relu"]))
     assert ka == base                                 # ReLU needs no arguments
@@ -291,10 +390,10 @@ def test_operand_size_limits(layout):
     assert name(below) == f"t0g_gemm_256x256_k64_{layout.lower()}_bf16"
     for m in ((1 << 30) // k, (1 << 31) // k, (1 << 34) // k):                    # 1 GiB .. 32 GiB of A
         assert name(m) == f"t0g_gemm_256x256_k64_{layout.lower()}_bf16_x", m
-    c128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    c128 = t0g.GemmConfig.preset("gfx950_128x128_k64")
     assert name((1 << 31) // k, config=c128).endswith("_bf16_x")                   # forced onto 256x256
     assert name((1 << 31) // k, config=c128.copy(split_k=2)) == f"t0g_gemm_256x256_k64_{layout.lower()}_f32_x"
-    sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+    sk = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
     assert name((1 << 31) // k, config=sk).endswith("_bf16_x")                     # no wide stream-K kernel
     # unaligned A: element-wise, refused once A spans 2^31 elements
     assert name((1 << 31) // k - 8, a=a + 2).endswith("_u")

@@ -94,7 +94,7 @@ def test_tile_abi_split_with_epilogue_chain(rt):
     """A split tile kernel with a chain: the library reduces the planes in plane order
     and applies the chain once (bias is not added per plane)."""
     m, k, n = 128, 4096, 1024
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=8)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(split_k=8)
     chain = t0g.epilogue_chain(["bias", "relu"])
     kern = rt.ensure_tile_kernel(cfg, chain)
     x = o.rand_bf16_lcg(m * k, 3)
@@ -172,7 +172,7 @@ def test_compile_load_dispatch(rt, layout, m, n, k, sk):
     b_st = b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T)
     ref = o.gemm("NT", a_mk, b_nk, m, n, k)
     da, db = rt.upload(a_st), rt.upload(b_st)
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=sk) if sk else None
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(split_k=sk) if sk else None
     planes = max(sk, 1)
     dc = rt.alloc(planes * m * n * 4)
     try:
@@ -192,7 +192,7 @@ def test_compile_load_dispatch(rt, layout, m, n, k, sk):
 def test_dispatch_async_then_wait_idle(rt):
     """dispatch_async enqueues and returns; wait_idle waits for all of them
     (gpu_context.rs:332-384).  Eight GEMMs into eight outputs, one wait."""
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64")
     kern = rt.ensure_gemm_kernel(cfg)
     m, k, n = 128, 256, 192
     outs, refs, ins = [], [], []
@@ -227,7 +227,7 @@ def test_stream_k_wait_that_gives_up_poisons_the_device():
         a = r.upload(o.rand_bf16_xorshift(m * k, 5))
         b = r.upload(o.rand_bf16_xorshift(k * n, 6))
         c = r.alloc(m * n * 4)
-        sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+        sk = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
         r.gemm(a, b, c, m, n, k, transpose="NN", config=sk)   # a normal launch first: no error
         r.wait_idle()
         assert r.stream_k_timeouts() == 0
@@ -268,7 +268,7 @@ def test_gemm_group_workspace_growth_on_the_device_stream():
             bufs.append(a)
             return a
 
-        cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+        cfg = t0g.GemmConfig.preset("gfx950_64x64_k64").copy(split_k=4)
         sm, sn, sk_ = 128, 128, 2048                      # small: 4 planes x 64 KB
         x_s = o.rand_bf16_lcg(sm * sk_, 1)
         w_s = o.rand_bf16_lcg(sn * sk_, 2)
@@ -331,7 +331,7 @@ def test_stream_switch_orders_split_k_launches():
             bufs.append(a)
             return a
 
-        cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+        cfg = t0g.GemmConfig.preset("gfx950_64x64_k64").copy(split_k=4)
         bm, bn, bk = 1024, 1024, 8192
         sm, sn, sk_ = 256, 256, 4096
         x_b, w_b = o.rand_bf16_lcg(bm * bk, 21), o.rand_bf16_lcg(bn * bk, 22)
@@ -458,11 +458,11 @@ def test_tune_tile_ir_on_the_thin_shape(rt, tmp_path):
 # ---- workgroup timeline (diagnostic) -------------------------------------------
 
 @pytest.mark.parametrize("preset,m,n,k,sk,layout", [
-    ("tile_256x256_k64", 1024, 768, 512, 0, "NN"),      # 12 workgroups, 8-wave ping-pong kernel
-    ("tile_256x256_k64", 512, 768, 384, 0, "NT"),       # 6 workgroups, 8-wave ping-pong kernel
-    ("tile_256x256_k64", 512, 512, 384, 0, "TN"),       # 4 workgroups, 4-wave kernel
-    ("tile_128x128_k64", 256, 640, 1024, 4, "NT"),      # 10 tiles x 4 K slices, deep-ring kernel
-    ("tile_64x64_k64", 1024, 1024, 128, 0, "NN"),       # 256 workgroups, 4-stage ring kernel
+    ("gfx950_256x256_k64", 1024, 768, 512, 0, "NN"),      # 12 workgroups, 8-wave ping-pong kernel
+    ("gfx950_256x256_k64", 512, 768, 384, 0, "NT"),       # 6 workgroups, 8-wave ping-pong kernel
+    ("gfx950_256x256_k64", 512, 512, 384, 0, "TN"),       # 4 workgroups, 4-wave kernel
+    ("gfx950_128x128_k64", 256, 640, 1024, 4, "NT"),      # 10 tiles x 4 K slices, deep-ring kernel
+    ("gfx950_64x64_k64", 1024, 1024, 128, 0, "NN"),       # 256 workgroups, 4-stage ring kernel
 ])
 def test_timeline_records_every_workgroup(rt, preset, m, n, k, sk, layout):
     """With t0g_set_timeline on, launches run the instrumented build of the kernels

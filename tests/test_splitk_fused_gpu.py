@@ -23,9 +23,9 @@ import t0g
 
 pytestmark = pytest.mark.gpu
 
-P128 = t0g.GemmConfig.preset("tile_128x128_k64")
-P256 = t0g.GemmConfig.preset("tile_256x256_k64")
-P64 = t0g.GemmConfig.preset("tile_64x64_k64")
+P128 = t0g.GemmConfig.preset("gfx950_128x128_k64")
+P256 = t0g.GemmConfig.preset("gfx950_256x256_k64")
+P64 = t0g.GemmConfig.preset("gfx950_64x64_k64")
 
 
 def _log(msg):

@@ -60,10 +60,10 @@ def test_each_workgroup_leaves_at_most_one_partial(tiles, ipt):
 
 
 def test_stream_k_config_rules():
-    cfg = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
     cfg.validate()
     assert cfg.name() == "t0_gemm_256x256_k64_ldsdb_streamk"
-    for preset in ("tile_128x128_k64", "tile_64x64_k64"):
+    for preset in ("gfx950_128x128_k64", "gfx950_64x64_k64"):
         bad = t0g.GemmConfig.preset(preset).copy(split_k=t0g.STREAM_K)
         with pytest.raises(t0g.T0gError) as e:
             bad.validate()
@@ -79,7 +79,7 @@ def test_stream_k_config_rules():
 
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 def test_stream_k_plan(layout):
-    cfg = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
     m, n, k = 1024, 11008, 4096
     a, b = 1 << 20, 1 << 30
     d = t0g.gemm_desc(a, b, 0, m, n, k, transpose=layout, out_dtype=t0g.BF16, config=cfg)
@@ -94,7 +94,7 @@ def test_stream_k_plan(layout):
     z = t0g.gemm_desc(a, b, 0, m, n, 0, transpose=layout, config=cfg)
     assert not t0g.gemm_kernel_name(z).endswith("_sk")
     # forcing it through desc.split_k on a 128x128 config is refused
-    c128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    c128 = t0g.GemmConfig.preset("gfx950_128x128_k64")
     with pytest.raises(t0g.T0gError):
         t0g.gemm_kernel_name(t0g.gemm_desc(a, b, 0, m, n, k, transpose=layout, config=c128, split_k=t0g.STREAM_K))
 

@@ -13,8 +13,8 @@ import t0g
 
 pytestmark = pytest.mark.gpu
 
-SK = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
-DP = t0g.GemmConfig.preset("tile_256x256_k64")
+SK = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
+DP = t0g.GemmConfig.preset("gfx950_256x256_k64")
 
 
 def _log(msg):

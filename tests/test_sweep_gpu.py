@@ -26,7 +26,7 @@ import os
 # one-off correctness runs; the default is the committed 48-case sweep.
 N_CASES = int(os.environ.get("T0G_SWEEP_CASES", "48"))
 SEED0 = int(os.environ.get("T0G_SWEEP_SEED0", "1000"))
-PRESETS = [None, "tile_256x256_k64", "tile_128x128_k64", "tile_64x64_k64"]
+PRESETS = [None, "gfx950_256x256_k64", "gfx950_128x128_k64", "gfx950_64x64_k64"]
 
 
 def _log(msg):

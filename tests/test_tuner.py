@@ -45,7 +45,7 @@ def test_params_are_settable_and_checked(tmp_path):
 def test_cache_roundtrip(tmp_path):
     """test_cache_roundtrip (auto_gemm.rs:580-610): save, then a new tuner on the same
     directory loads the same config and TFLOPS, marked from_cache, with its ranking."""
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=4)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(split_k=4)
     ranking = [(cfg.name(), 79.2), ("t0_gemm_64x64_k64_ldsdb", 65.3)]
     with _tuner(tmp_path) as t:
         t.save_cache(4096, 4096, 4096, cfg, 79.2, ranking)
@@ -66,7 +66,7 @@ def test_cache_roundtrip(tmp_path):
 def test_cache_file_keeps_the_reference_keys(tmp_path):
     """The file holds every key save_cache writes (auto_gemm.rs:373-386), parseable as
     JSON, plus the architecture, layout, output type and size."""
-    cfg = t0g.GemmConfig.preset("tile_256x256_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64")
     with _tuner(tmp_path) as t:
         t.save_cache(1024, 11008, 4096, cfg, 991.44, [(cfg.name(), 991.44)])
     path = tmp_path / "cache" / "gemm_1024x11008x4096.json"
@@ -81,7 +81,7 @@ def test_cache_file_keeps_the_reference_keys(tmp_path):
 
 
 def test_file_names_per_layout_and_output(tmp_path):
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64")
     with _tuner(tmp_path) as t:
         t.save_cache(64, 128, 256, cfg, 1.0, transpose="NN", out_dtype=t0g.BF16)
         t.save_cache(64, 128, 256, cfg, 2.0, transpose="TN")
@@ -148,7 +148,7 @@ def test_broken_ranking_keeps_the_config(tmp_path):
 
 def test_invalidate_and_clear(tmp_path):
     """invalidate / clear (auto_gemm.rs:393-403); clear leaves files it did not write."""
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64")
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64")
     with _tuner(tmp_path) as t:
         t.save_cache(256, 256, 256, cfg, 1.0)
         t.save_cache(512, 512, 512, cfg, 2.0)
@@ -168,15 +168,15 @@ def test_invalidate_and_clear(tmp_path):
 
 def test_store_rejects_bad_input(tmp_path):
     with _tuner(tmp_path) as t:
-        bad = t0g.GemmConfig.preset("tile_128x128_k64").copy(tile_m=96)
+        bad = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(tile_m=96)
         with pytest.raises(t0g.T0gError) as e:
             t.save_cache(64, 64, 64, bad, 1.0)
         assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG
         with pytest.raises(t0g.T0gError) as e:
-            t.save_cache(0, 64, 64, t0g.GemmConfig.preset("tile_64x64_k64"), 1.0)
+            t.save_cache(0, 64, 64, t0g.GemmConfig.preset("gfx950_64x64_k64"), 1.0)
         assert e.value.code == t0g.ERR_INVALID_ARG
         with pytest.raises(t0g.T0gError):
-            t.save_cache(64, 64, 64, t0g.GemmConfig.preset("tile_64x64_k64"), 1.0, [('a"b', 1.0)])
+            t.save_cache(64, 64, 64, t0g.GemmConfig.preset("gfx950_64x64_k64"), 1.0, [('a"b', 1.0)])
         with pytest.raises(t0g.T0gError):
             t.lookup(64, 64, 64, transpose=7)
 
@@ -185,7 +185,7 @@ def test_unwritable_directory_is_an_error_for_store(tmp_path):
     (tmp_path / "file").write_text("x")
     with t0g.GemmTuner.with_cache_dir(tmp_path / "file" / "sub") as t:
         with pytest.raises(t0g.T0gError):
-            t.save_cache(64, 64, 64, t0g.GemmConfig.preset("tile_64x64_k64"), 1.0)
+            t.save_cache(64, 64, 64, t0g.GemmConfig.preset("gfx950_64x64_k64"), 1.0)
 
 
 SHAPES = [(256, 256, 256), (4096, 4096, 4096), (8192, 8192, 8192), (128, 4096, 4096), (256, 256, 32768),
@@ -220,7 +220,7 @@ def test_candidates_cover_every_tile():
 def test_tile_ir_cache_roundtrip(tmp_path):
     """save_tile_ir_cache then load_tile_ir_cache on a new tuner: the same tile, split
     and TFLOPS, from_cache, the TileGemm-named ranking (cost_model.rs:1076-1093)."""
-    cfg = t0g.GemmConfig.preset("tile_128x128_k64").copy(split_k=8)
+    cfg = t0g.GemmConfig.preset("gfx950_128x128_k64").copy(split_k=8)
     ranking = [(t0g.tile_config_name(cfg), 271.3), ("tile_gemm_64x64_k64_db_sk2", 200.0)]
     with _tuner(tmp_path) as t:
         t.save_tile_ir_cache(128, 4096, 4096, cfg, 271.3, ranking)
@@ -272,7 +272,7 @@ def test_tile_ir_bad_files_are_misses(tmp_path, text):
 
 def test_tile_ir_store_refuses_stream_k(tmp_path):
     with _tuner(tmp_path) as t:
-        sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
+        sk = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
         with pytest.raises(t0g.T0gError) as e:
             t.save_tile_ir_cache(4352, 4096, 8192, sk, 1.0)
         assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG

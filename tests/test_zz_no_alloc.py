@@ -130,11 +130,11 @@ def test_noalloc_matches_gemm_two_calls_in_a_row(rt, first, second):
 def test_noalloc_forced_split_and_stream_k(rt):
     """A forced split (planes in the scratch) and a stream-K config (data-parallel here):
     each equal to t0g_gemm with the same plan."""
-    p128 = t0g.GemmConfig.preset("tile_128x128_k64")
+    p128 = t0g.GemmConfig.preset("gfx950_128x128_k64")
     r_gemm, r_noalloc, ref32 = _pair(rt, "NT", 512, 384, 4096, 41, cfg=p128, out=t0g.F32, split_k=8)
     _check(r_gemm, r_noalloc, ref32, 4096, t0g.F32, "forced split 8")
-    sk = t0g.GemmConfig.preset("tile_256x256_k64").copy(split_k=t0g.STREAM_K)
-    dp = t0g.GemmConfig.preset("tile_256x256_k64")
+    sk = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
+    dp = t0g.GemmConfig.preset("gfx950_256x256_k64")
     m, n, k = 1024, 768, 2048
     a = o.rand_bf16_lcg(m * k, 43)
     b = o.rand_bf16_lcg(k * n, 44)
@@ -157,7 +157,7 @@ def test_noalloc_caller_workspace(rt):
     m, n, k = 256, 512, 8192
     a = o.rand_bf16_lcg(m * k, 51)
     b = o.rand_bf16_lcg(n * k, 52)
-    cfg = t0g.GemmConfig.preset("tile_64x64_k64").copy(split_k=4)
+    cfg = t0g.GemmConfig.preset("gfx950_64x64_k64").copy(split_k=4)
     da, db = rt.upload(a), rt.upload(b)
     c, ws = rt.alloc(m * n * 4), rt.alloc(4 * m * n * 4)
     try:
@@ -177,7 +177,7 @@ def test_noalloc_refuses_more_scratch_than_it_has(rt):
     """4096 x 4096 with 8 planes needs 512 MiB: refused before anything is launched,
     and the device stays usable."""
     d = t0g.gemm_desc(1 << 20, 1 << 21, 1 << 22, 4096, 4096, 4096,
-                      config=t0g.GemmConfig.preset("tile_128x128_k64"), split_k=8)
+                      config=t0g.GemmConfig.preset("gfx950_128x128_k64"), split_k=8)
     with pytest.raises(t0g.T0gError) as e:
         gemm_noalloc(rt, d)
     assert e.value.code == t0g.ERR_INVALID_ARG and "scratch" in str(e.value)
