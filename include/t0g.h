@@ -370,9 +370,14 @@ T0G_API int t0g_gemm(t0g_device *dev, const t0g_gemm_desc *desc);
  * holds on each GPU it runs on until the process ends (a problem needing more
  * returns T0G_ERR_INVALID_ARG).  Stream-K configs run the data-parallel schedule
  * of the same tile.  Every call on one GPU shares that GPU's scratch, which keeps
- * the last call's partial sums: calls in the same stream are ordered, but calls
- * that overlap on one GPU (other streams or device handles) race on it. */
+ * the last call's partial sums. */
 #define T0G_NOALLOC_SCRATCH_BYTES (64u << 20)
+/* Calls that put planes in the scratch are taken one after another across all
+ * handles and streams of a GPU (each waits for an event the previous one
+ * recorded; no allocation), except under stream capture, where an event from
+ * outside the capture cannot be waited for: captured calls on one GPU must be
+ * ordered by the caller.  The instrumented timeline build is never used here
+ * (loading it would allocate). */
 T0G_API int t0g_gemm_noalloc(t0g_device *dev, const t0g_gemm_desc *desc);
 /* Enqueue n GEMMs that do not depend on each other (no output of one is an
  * input or output of another) to run concurrently: round-robin over the device
@@ -440,6 +445,31 @@ T0G_API int t0g_matmul_backward_weight_f32(t0g_device *dev, uint64_t x, uint64_t
  * bf16(X[M,K]) * WT[N,K]^T with WT already bf16. */
 T0G_API int t0g_matmul_wt_bf16_f32(t0g_device *dev, uint64_t x, uint64_t wt_bf16, uint64_t y, uint32_t m,
                                    uint32_t k, uint32_t n);
+
+/* GpuRuntime's bf16 weight cache (src/ignis/gpu_context.rs:100, 385-433), per
+ * device handle.  get_or_create_bf16(tensor_id, f32_buf, n, convert_kernel):
+ * the first call for tensor_id converts n f32 at f32_addr (t0g_f32_to_bf16's
+ * rounding) into a buffer the cache owns and returns its device address; later
+ * calls return that buffer without converting (the reference keys on the id
+ * alone; a call with another n is refused with T0G_ERR_INVALID_ARG).  The
+ * buffer stays valid until the id is invalidated or the cache cleared
+ * (invalidate_bf16 / clear_bf16_cache: call after a weight update); t0g_free
+ * and t0g_recycle refuse it.  Invalidated buffers go back to the handle's
+ * pool, in device-stream order, so a training step's invalidate + get
+ * reconverts into the same memory without a hipMalloc. */
+T0G_API int t0g_bf16_cache_get(t0g_device *dev, uint64_t tensor_id, uint64_t f32_addr, size_t n,
+                               uint64_t *bf16_addr);
+T0G_API int t0g_bf16_cache_invalidate(t0g_device *dev, uint64_t tensor_id);
+T0G_API int t0g_bf16_cache_clear(t0g_device *dev);
+/* Cached tensors and the pool bytes they hold (no reference counterpart). */
+T0G_API int t0g_bf16_cache_stats(t0g_device *dev, uint64_t *entries, uint64_t *bytes);
+/* t0g_matmul_f32 / t0g_matmul_backward_data_f32 with W's bf16 copy taken from
+ * the cache under w_id (converted on the first call only); X (dY) is
+ * converted every call.  The caller invalidates w_id when W changes. */
+T0G_API int t0g_matmul_f32_cached(t0g_device *dev, uint64_t x, uint64_t w, uint64_t w_id, uint64_t y,
+                                  uint32_t m, uint32_t k, uint32_t n);
+T0G_API int t0g_matmul_backward_data_f32_cached(t0g_device *dev, uint64_t dy, uint64_t w, uint64_t w_id,
+                                                uint64_t dx, uint32_t m, uint32_t k, uint32_t n);
 
 /* ---- GEMM autotuner and its on-disk cache ----------------------------------- *
  * GemmTuner (src/t0/auto_gemm.rs:28-417): benchmark the model's best candidate
@@ -580,6 +610,11 @@ T0G_API int t0g_set_timeline(int on);
 T0G_API int t0g_timeline_read(t0g_device *dev, uint64_t *out, size_t entries, size_t *written);
 /* Zero the device's timeline array (entries of workgroups that did not run stay 0). */
 T0G_API int t0g_timeline_clear(t0g_device *dev);
+/* Device-memory allocations this library has asked HIP for, process-wide
+ * (every hipMalloc and every code-object load, which places the code in device
+ * memory); lets a test show that an entry point such as t0g_gemm_noalloc
+ * allocates nothing.  No reference counterpart. */
+T0G_API int t0g_debug_device_alloc_count(uint64_t *count);
 /* Make the n-th HIP call from now (n >= 1) fail with a simulated error;
  * n = 0 disarms.  Lets the error mapping and poisoning be tested without a
  * real device fault. */

@@ -4,8 +4,11 @@
 
 #include <stdint.h>
 
+#include <functional>
 #include <string>
 #include <vector>
+
+#include <hip/hip_runtime_api.h>
 
 #include "t0g.h"
 
@@ -86,6 +89,11 @@ int read_kernel_meta(const void *code_object, size_t size, const char *symbol, K
 // Device address of device `ordinal`'s copy of the no-allocation scratch array
 // (t0g_noalloc.hip); the device must be current on the first call for it.
 int noalloc_scratch(int ordinal, uint64_t *ptr);
+// Run `launch` (work on `stream` that uses device `ordinal`'s scratch) after the
+// previous such work on any stream of that device, and record its end for the
+// next one; under stream capture the caller orders the calls.  noalloc_scratch
+// must have succeeded for the device.
+int noalloc_scratch_use(int ordinal, hipStream_t stream, const std::function<int()> &launch);
 
 }  // namespace t0g
 

@@ -15,6 +15,7 @@
 // every element of the fp32 planes before the reduce kernel reads it.
 #include <hip/hip_runtime.h>
 
+#include <functional>
 #include <mutex>
 
 #include "t0g.h"
@@ -30,6 +31,11 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 uint64_t g_ptr[kMaxDevices];
+// Per device: the event recorded after the last call that used the scratch, and
+// the lock that makes "wait for it, launch, record it" one step, so calls from
+// different handles or streams take the scratch one after another.
+hipEvent_t g_last[kMaxDevices];
+std::mutex g_use[kMaxDevices];
 
 }  // namespace
 
@@ -46,9 +52,35 @@ int noalloc_scratch(int ordinal, uint64_t *ptr) {
         if (e != hipSuccess || !p)
             return fail(T0G_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s (%d)", ordinal,
                         hipGetErrorString(e), (int)e);
+        hipEvent_t ev = nullptr;
+        const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e2 != hipSuccess)
+            return fail(T0G_ERR_HIP, "hipEventCreateWithFlags (scratch order) on device %d failed: %s (%d)", ordinal,
+                        hipGetErrorString(e2), (int)e2);
+        g_last[ordinal] = ev;
         g_ptr[ordinal] = (uint64_t)p;
     }
     *ptr = g_ptr[ordinal];
+    return T0G_OK;
+}
+
+int noalloc_scratch_use(int ordinal, hipStream_t stream, const std::function<int()> &launch) {
+    std::lock_guard<std::mutex> lk(g_use[ordinal]);
+    // Under stream capture the graph orders its own nodes; an event recorded outside
+    // the capture cannot be waited for inside it, so the caller orders captured calls.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    hipEvent_t ev = g_last[ordinal];
+    if (!capturing) {
+        const hipError_t e = hipStreamWaitEvent(stream, ev, 0);
+        if (e != hipSuccess)
+            return fail(T0G_ERR_HIP, "hipStreamWaitEvent (scratch order) failed: %s (%d)", hipGetErrorString(e), (int)e);
+    }
+    int rc = launch();
+    if (rc || capturing) return rc;
+    const hipError_t e = hipEventRecord(ev, stream);
+    if (e != hipSuccess)
+        return fail(T0G_ERR_HIP, "hipEventRecord (scratch order) failed: %s (%d)", hipGetErrorString(e), (int)e);
     return T0G_OK;
 }
 

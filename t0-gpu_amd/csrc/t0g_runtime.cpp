@@ -92,6 +92,15 @@ struct t0g_device {
     size_t ws_bytes = 0;
     uint64_t conv = 0;         // bf16 operand scratch of the matmul entry points
     size_t conv_bytes = 0;
+    // GpuRuntime::bf16_cache (src/ignis/gpu_context.rs:100): tensor id -> its bf16 copy.
+    // The buffers come from the pool but belong to the cache (not to `allocations`, so
+    // t0g_free / t0g_recycle refuse them); invalidating an id returns its buffer to the pool.
+    struct Bf16Copy {
+        uint64_t addr;
+        size_t n;       // elements converted
+        size_t bytes;   // pool size of the buffer
+    };
+    std::unordered_map<uint64_t, Bf16Copy> bf16_cache;
     uint32_t num_cus = 0;      // compute units: the stream-K grid
     uint64_t scratch = 0;      // this device's no-allocation scratch (0: unavailable, see scratch_error)
     std::string scratch_error;
@@ -136,6 +145,21 @@ static bool injected_failure() {
 }
 
 #define T0G_HIP(expr) (::t0g::injected_failure() ? hipErrorLaunchFailure : (expr))
+
+// Device-memory allocations this library has asked HIP for (hipMalloc and
+// code-object loads), process-wide, so a test can show that an entry point
+// allocates nothing.
+static std::atomic<uint64_t> g_device_allocs{0};
+
+static hipError_t dev_malloc(void **p, size_t bytes) {
+    g_device_allocs.fetch_add(1);
+    return hipMalloc(p, bytes);
+}
+
+static hipError_t module_load(hipModule_t *m, const void *image) {
+    g_device_allocs.fetch_add(1);
+    return hipModuleLoadData(m, image);
+}
 
 static int hip_fail(hipError_t e, const char *what) {
     return fail(e == hipErrorOutOfMemory ? T0G_ERR_OUT_OF_MEMORY : T0G_ERR_HIP, "%s failed: %s (%d)", what,
@@ -210,7 +234,7 @@ static int wait_stream(t0g_device *dev) {
 
 static int load_timeline_module(t0g_device *dev) {
     if (dev->module_tl) return T0G_OK;
-    hipError_t e = T0G_HIP(hipModuleLoadData(&dev->module_tl, t0g_hsaco_tl_begin));
+    hipError_t e = T0G_HIP(module_load(&dev->module_tl, t0g_hsaco_tl_begin));
     if (e != hipSuccess) {
         dev->module_tl = nullptr;
         return hip_fail(e, "hipModuleLoadData(timeline code object)");
@@ -395,7 +419,7 @@ static int ensure_workspace(t0g_device *dev, size_t bytes) {
         if (e != hipSuccess) return poison(dev, hip_fail(e, "hipFree(workspace)"));
     }
     void *p = nullptr;
-    hipError_t e = T0G_HIP(hipMalloc(&p, bytes));
+    hipError_t e = T0G_HIP(dev_malloc(&p, bytes));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
     dev->ws = (uint64_t)p;
     dev->ws_bytes = bytes;
@@ -420,7 +444,7 @@ static int ensure_sk_sync(t0g_device *dev) {
     const size_t bytes =
         (T0G_SK_CTL_WORDS + std::max<size_t>(kNumCUs, (size_t)T0G_RED_LINE_WORDS * (T0G_RED_MAX_GRID / 2))) * 4;
     void *ptr = nullptr;
-    hipError_t e = T0G_HIP(hipMalloc(&ptr, bytes));
+    hipError_t e = T0G_HIP(dev_malloc(&ptr, bytes));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(stream-K flags)");
     e = T0G_HIP(hipMemsetAsync(ptr, 0, bytes, dev->stream));
     if (e != hipSuccess) {
@@ -434,7 +458,10 @@ static int ensure_sk_sync(t0g_device *dev) {
 // The GEMM kernel's argument block for a plan.  With splits > 1 and no
 // caller-owned planes (o.c_split_stride == 0) the kernel writes fp32 planes to
 // `ws` and *reduce is set: the reduce kernel then produces C.
-static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws, T0gGemmArgs *out, bool *reduce_out) {
+// allow_timeline = false: never the instrumented code object (its first use loads
+// a module, which allocates device memory).
+static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws, T0gGemmArgs *out, bool *reduce_out,
+                           bool allow_timeline = true) {
     T0gGemmArgs &args = *out;
     memset(&args, 0, sizeof args);
     args.a = o.a;
@@ -448,7 +475,7 @@ static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws
     args.tiles_m = p.tiles_m;
     args.tiles_n = p.tiles_n;
     args.group_m = 8;
-    args.flags = T0G_FLAG_XCD_REMAP | (g_timeline.load() ? T0G_FLAG_TIMELINE : 0u);
+    args.flags = T0G_FLAG_XCD_REMAP | (allow_timeline && g_timeline.load() ? T0G_FLAG_TIMELINE : 0u);
     const bool reduce = p.splits > 1 && o.c_split_stride == 0 && !p.fused;
     if (reduce) {
         args.c = ws;
@@ -474,10 +501,11 @@ static void fill_gemm_args(const GemmPlan &p, const GemmOperands &o, uint64_t ws
 
 // Launch the plan's GEMM kernel.  With splits > 1 and no caller-owned planes
 // the partial planes go to `ws` and the reduce kernel produces C.
-static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws) {
+static int run_plan(t0g_device *dev, const GemmPlan &p, const GemmOperands &o, uint64_t ws,
+                    bool allow_timeline = true) {
     T0gGemmArgs args;
     bool reduce = false;
-    fill_gemm_args(p, o, ws, &args, &reduce);
+    fill_gemm_args(p, o, ws, &args, &reduce, allow_timeline);
     hipFunction_t f = nullptr;
     int rc = get_function(dev, p.symbol, &f, (args.flags & T0G_FLAG_TIMELINE) != 0);
     if (rc) return rc;
@@ -630,6 +658,12 @@ int t0g_stream_k_timeouts(t0g_device *dev, uint32_t *count) {
     return ok();
 }
 
+int t0g_debug_device_alloc_count(uint64_t *count) {
+    if (!count) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    *count = g_device_allocs.load();
+    return ok();
+}
+
 int t0g_debug_fail_hip_call(int n) {
     if (n < 0) return fail(T0G_ERR_INVALID_ARG, "n must be >= 0");
     g_fail_countdown.store(n);
@@ -744,7 +778,7 @@ int t0g_device_open(int ordinal, t0g_device **out) {
         dev->scratch = 0;
         dev->scratch_error = g_last_error;
     }
-    if ((e = T0G_HIP(hipModuleLoadData(&dev->module, t0g_hsaco_begin))) != hipSuccess) {
+    if ((e = T0G_HIP(module_load(&dev->module, t0g_hsaco_begin))) != hipSuccess) {
         (void)hipStreamDestroy(dev->own_stream);
         return hip_fail(e, "hipModuleLoadData(gfx950 GEMM code object)");
     }
@@ -769,6 +803,7 @@ int t0g_device_close(t0g_device *dev) {
     }
     if (dev->fork_ev) (void)hipEventDestroy(dev->fork_ev);
     for (const auto &a : dev->allocations) (void)hipFree((void *)a.first);
+    for (const auto &c : dev->bf16_cache) (void)hipFree((void *)c.second.addr);
     for (const auto &bucket : dev->pool)
         for (uint64_t a : bucket.second) (void)hipFree((void *)a);
     for (hipModule_t m : dev->extra_modules) (void)hipModuleUnload(m);
@@ -799,6 +834,9 @@ int t0g_device_set_stream(t0g_device *dev, void *hip_stream) {
             return hip_fail(e, "hipEventRecord");
         if ((e = T0G_HIP(hipStreamWaitEvent(next, dev->order_event, 0))) != hipSuccess)
             return hip_fail(e, "hipStreamWaitEvent");
+        // A stream-K launch whose timeout count is not yet checked is now ordered
+        // before everything on the new stream, so the new stream's waits check it.
+        if (dev->sk_stream == dev->stream) dev->sk_stream = next;
     }
     dev->stream = next;
     return ok();
@@ -829,7 +867,7 @@ static int alloc_locked(t0g_device *dev, size_t bytes, uint64_t *addr) {
         dev->pool_hits++;
     } else {
         void *p = nullptr;
-        hipError_t e = T0G_HIP(hipMalloc(&p, size));
+        hipError_t e = T0G_HIP(dev_malloc(&p, size));
         if (e != hipSuccess) return hip_fail(e, "hipMalloc");
         *addr = (uint64_t)p;
         dev->pool_misses++;
@@ -1063,7 +1101,7 @@ int t0g_kernel_load(t0g_device *dev, const void *code_object, size_t size, const
     std::lock_guard<std::mutex> lk(dev->mu);
     if ((rc = check_usable(dev))) return rc;
     hipModule_t m = nullptr;
-    hipError_t e = T0G_HIP(hipModuleLoadData(&m, code_object));
+    hipError_t e = T0G_HIP(module_load(&m, code_object));
     if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
     hipFunction_t f = nullptr;
     e = T0G_HIP(hipModuleGetFunction(&f, m, symbol));
@@ -1488,7 +1526,12 @@ int t0g_gemm_noalloc(t0g_device *dev, const t0g_gemm_desc *d) {
             ws = dev->scratch;
         }
     }
-    if ((rc = run_plan(dev, p, o, ws))) return rc;
+    // never the timeline build: its first use loads a code object, which allocates
+    if (ws != 0 && ws == dev->scratch)
+        rc = noalloc_scratch_use(dev->ordinal, dev->stream, [&] { return run_plan(dev, p, o, ws, false); });
+    else
+        rc = run_plan(dev, p, o, ws, false);
+    if (rc) return rc;
     return ok();
 }
 
@@ -1646,7 +1689,7 @@ static int ensure_conv(t0g_device *dev, size_t bytes) {
         if (e != hipSuccess) return poison(dev, hip_fail(e, "hipFree(conversion scratch)"));
     }
     void *p = nullptr;
-    hipError_t e = T0G_HIP(hipMalloc(&p, bytes));
+    hipError_t e = T0G_HIP(dev_malloc(&p, bytes));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(conversion scratch)");
     dev->conv = (uint64_t)p;
     dev->conv_bytes = bytes;
@@ -1717,6 +1760,115 @@ int t0g_matmul_wt_bf16_f32(t0g_device *dev, uint64_t x, uint64_t wt_bf16, uint64
     // Y = X * WT^T with WT [N][K] bf16 -> NT; only X needs converting.
     int rc = matmul_common(dev, x, (size_t)m * k, wt_bf16, 0, y, m, n, k, T0G_NT);
     return rc ? rc : ok();
+}
+
+// ---- bf16 weight cache (GpuRuntime::get_or_create_bf16 and friends) ----------
+
+// The cached bf16 copy of tensor `id`, converting n f32 at f32_addr on a miss.
+static int bf16_cache_get_locked(t0g_device *dev, uint64_t id, uint64_t f32_addr, size_t n, uint64_t *out) {
+    auto it = dev->bf16_cache.find(id);
+    if (it != dev->bf16_cache.end()) {
+        if (it->second.n != n)
+            return fail(T0G_ERR_INVALID_ARG,
+                        "tensor %llu is cached with %zu elements, asked for %zu (invalidate it after a resize)",
+                        (unsigned long long)id, it->second.n, n);
+        *out = it->second.addr;
+        return T0G_OK;
+    }
+    uint64_t addr = 0;
+    int rc = alloc_locked(dev, round256(n * 2), &addr);
+    if (rc) return rc;
+    const size_t bytes = dev->allocations[addr];
+    dev->allocations.erase(addr);   // owned by the cache from here on
+    if ((rc = convert_locked(dev, f32_addr, addr, n))) {
+        dev->pool[bytes].push_back(addr);
+        dev->pool_bytes += bytes;
+        return rc;
+    }
+    dev->bf16_cache[id] = t0g_device::Bf16Copy{addr, n, bytes};
+    *out = addr;
+    return T0G_OK;
+}
+
+static void bf16_cache_drop_locked(t0g_device *dev, std::unordered_map<uint64_t, t0g_device::Bf16Copy>::iterator it) {
+    // Back to the pool: work already queued on the device stream may still read it, and a
+    // later owner uses it in that stream's order.
+    dev->pool[it->second.bytes].push_back(it->second.addr);
+    dev->pool_bytes += it->second.bytes;
+    dev->bf16_cache.erase(it);
+}
+
+int t0g_bf16_cache_get(t0g_device *dev, uint64_t tensor_id, uint64_t f32_addr, size_t n, uint64_t *bf16_addr) {
+    if (!dev || !bf16_addr) return fail(T0G_ERR_INVALID_ARG, "NULL argument");
+    if (!f32_addr || n == 0) return fail(T0G_ERR_INVALID_ARG, "empty tensor");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if ((rc = bf16_cache_get_locked(dev, tensor_id, f32_addr, n, bf16_addr))) return rc;
+    return ok();
+}
+
+int t0g_bf16_cache_invalidate(t0g_device *dev, uint64_t tensor_id) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    auto it = dev->bf16_cache.find(tensor_id);
+    if (it != dev->bf16_cache.end()) bf16_cache_drop_locked(dev, it);
+    return ok();
+}
+
+int t0g_bf16_cache_clear(t0g_device *dev) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    while (!dev->bf16_cache.empty()) bf16_cache_drop_locked(dev, dev->bf16_cache.begin());
+    return ok();
+}
+
+int t0g_bf16_cache_stats(t0g_device *dev, uint64_t *entries, uint64_t *bytes) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    uint64_t b = 0;
+    for (const auto &c : dev->bf16_cache) b += c.second.bytes;
+    if (entries) *entries = dev->bf16_cache.size();
+    if (bytes) *bytes = b;
+    return ok();
+}
+
+// matmul / gemm_backward_data with W's bf16 copy taken from the cache: only the
+// activation operand is converted per call.
+static int matmul_cached(t0g_device *dev, uint64_t a_f32, size_t a_elems, uint64_t w, uint64_t w_id, size_t w_elems,
+                         uint64_t c, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose) {
+    if (!dev) return fail(T0G_ERR_INVALID_ARG, "device is NULL");
+    if (!a_f32 || !w || !c) return fail(T0G_ERR_INVALID_ARG, "NULL operand");
+    std::lock_guard<std::mutex> lk(dev->mu);
+    int rc = check_usable(dev);
+    if (rc) return rc;
+    if (m == 0 || n == 0) return ok();
+    uint64_t w16 = 0;
+    if (w_elems && (rc = bf16_cache_get_locked(dev, w_id, w, w_elems, &w16))) return rc;
+    if ((rc = ensure_conv(dev, round256(a_elems * 2) + 256))) return rc;
+    if ((rc = convert_locked(dev, a_f32, dev->conv, a_elems))) return rc;
+    t0g_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = dev->conv;
+    d.b = w_elems ? w16 : dev->conv;   // K == 0: the GEMM reads no operand
+    d.c = c;
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.transpose = transpose;
+    d.out_dtype = T0G_F32;
+    if ((rc = gemm_locked(dev, &d))) return rc;
+    return ok();
+}
+
+int t0g_matmul_f32_cached(t0g_device *dev, uint64_t x, uint64_t w, uint64_t w_id, uint64_t y, uint32_t m, uint32_t k,
+                          uint32_t n) {
+    return matmul_cached(dev, x, (size_t)m * k, w, w_id, (size_t)k * n, y, m, n, k, T0G_NN);
+}
+
+int t0g_matmul_backward_data_f32_cached(t0g_device *dev, uint64_t dy, uint64_t w, uint64_t w_id, uint64_t dx,
+                                        uint32_t m, uint32_t k, uint32_t n) {
+    return matmul_cached(dev, dy, (size_t)m * n, w, w_id, (size_t)k * n, dx, m, k, n, T0G_NT);
 }
 
 }  // extern "C"

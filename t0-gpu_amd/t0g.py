@@ -279,6 +279,12 @@ _sig("t0g_matmul_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_backward_data_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_backward_weight_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
 _sig("t0g_matmul_wt_bf16_f32", ctypes.c_int, _p, _u64, _u64, _u64, _u32, _u32, _u32)
+_sig("t0g_bf16_cache_get", ctypes.c_int, _p, _u64, _u64, ctypes.c_size_t, ctypes.POINTER(_u64))
+_sig("t0g_bf16_cache_invalidate", ctypes.c_int, _p, _u64)
+_sig("t0g_bf16_cache_clear", ctypes.c_int, _p)
+_sig("t0g_bf16_cache_stats", ctypes.c_int, _p, ctypes.POINTER(_u64), ctypes.POINTER(_u64))
+_sig("t0g_matmul_f32_cached", ctypes.c_int, _p, _u64, _u64, _u64, _u64, _u32, _u32, _u32)
+_sig("t0g_matmul_backward_data_f32_cached", ctypes.c_int, _p, _u64, _u64, _u64, _u64, _u32, _u32, _u32)
 
 
 class TuneResult(ctypes.Structure):
@@ -326,6 +332,7 @@ _sig("t0g_tile_ir_store", ctypes.c_int, _p, ctypes.POINTER(TuneResult), ctypes.P
 _sig("t0g_stream_k_begin", _u32, _u32, _u32, _u32)
 _sig("t0g_stream_k_worker", _u32, _u32, _u32, _u32)
 _sig("t0g_stream_k_timeouts", ctypes.c_int, _p, _u32p)
+_sig("t0g_debug_device_alloc_count", ctypes.c_int, ctypes.POINTER(_u64))
 _sig("t0g_debug_fail_hip_call", ctypes.c_int, ctypes.c_int)
 _sig("t0g_set_wait_timeout_ms", ctypes.c_int, _u32)
 _sig("t0g_set_stream_k_spin_limit", ctypes.c_int, _u32)
@@ -546,6 +553,13 @@ TIMELINE_TICK_NS = 10.0   # the GPU's constant 100 MHz clock
 def set_timeline(on):
     """Record per-workgroup timelines of later GEMM launches (diagnostic)."""
     _check(_lib.t0g_set_timeline(1 if on else 0))
+
+
+def device_alloc_count():
+    """Device allocations (hipMalloc, code-object loads) the library has made in this process."""
+    c = _u64()
+    _check(_lib.t0g_debug_device_alloc_count(ctypes.byref(c)))
+    return c.value
 
 
 def debug_fail_hip_call(n):
@@ -780,6 +794,30 @@ class GpuRuntime:
     def matmul_wt_bf16_f32(self, x, wt_bf16, y, m, k, n):
         """matmul_with_wt_bf16: Y[M,N] = bf16(X[M,K]) WT[N,K]^T."""
         _check(_lib.t0g_matmul_wt_bf16_f32(self.handle, x, wt_bf16, y, m, k, n))
+
+    # GpuRuntime::{get_or_create_bf16, invalidate_bf16, clear_bf16_cache} (src/ignis/gpu_context.rs:385-433)
+    def get_or_create_bf16(self, tensor_id, f32_addr, n):
+        out = _u64()
+        _check(_lib.t0g_bf16_cache_get(self.handle, tensor_id, f32_addr, n, ctypes.byref(out)))
+        return out.value
+
+    def invalidate_bf16(self, tensor_id):
+        _check(_lib.t0g_bf16_cache_invalidate(self.handle, tensor_id))
+
+    def clear_bf16_cache(self):
+        _check(_lib.t0g_bf16_cache_clear(self.handle))
+
+    def bf16_cache_stats(self):
+        e, b = _u64(), _u64()
+        _check(_lib.t0g_bf16_cache_stats(self.handle, ctypes.byref(e), ctypes.byref(b)))
+        return e.value, b.value
+
+    def matmul_f32_cached(self, x, w, w_id, y, m, k, n):
+        """matmul with W's bf16 copy from the cache under w_id."""
+        _check(_lib.t0g_matmul_f32_cached(self.handle, x, w, w_id, y, m, k, n))
+
+    def matmul_backward_data_f32_cached(self, dy, w, w_id, dx, m, k, n):
+        _check(_lib.t0g_matmul_backward_data_f32_cached(self.handle, dy, w, w_id, dx, m, k, n))
 
 
 # ---- autotuner (src/t0/auto_gemm.rs) -----------------------------------------

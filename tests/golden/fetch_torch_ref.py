@@ -23,7 +23,9 @@ FILES = [
     "h_gate_f32ref.bin",     # X.float() @ W_gate.float().T, f32 [64,512]
     "h_up_f32ref.bin",       # X.float() @ W_up.float().T, f32 [64,512]
     "h_gate_bf16acc.bin",    # torch.mm(X, W_gate.T) in bf16, stored f32
+    "h_up_bf16acc.bin",      # torch.mm(X, W_up.T) in bf16, stored f32
     "y_bf16_f32acc.bin",     # S.float() @ W_down.float().T, f32 [64,256]
+    "y_bf16chain.bin",       # torch.mm(S, W_down.T) in bf16, stored f32 [64,256]
 ]
 
 

@@ -132,6 +132,42 @@ def test_torch_golden_through_gpu(rt, bufs):
     assert np.abs(cy - refy).max() < 1e-5
 
 
+BF16_GOLDENS = [("x.bin", (64, 256), "w_gate.bin", (512, 256), "h_gate_bf16acc.bin"),
+                ("x.bin", (64, 256), "w_up.bin", (512, 256), "h_up_bf16acc.bin"),
+                ("swiglu_bf16_trunc.bin", (64, 512), "w_down.bin", (256, 512), "y_bf16chain.bin")]
+
+
+@pytest.mark.parametrize("preset", [None, "gfx950_256x256_k64", "gfx950_128x128_k64", "gfx950_64x64_k64",
+                                    "tile_64x64_k16"])
+@pytest.mark.parametrize("a_name,a_shape,b_name,b_shape,gold", BF16_GOLDENS)
+def test_bf16_output_against_torch_bf16_gemm(rt, bufs, preset, a_name, a_shape, b_name, b_shape, gold):
+    """The kernels' bf16-output NT mode against torch's bf16 GEMM (torch.mm on bf16 operands,
+    h_gate/h_up_bf16acc and y_bf16chain; src/t0/precision_vs_torch.rs:115-118, 302-305):
+    within one bf16 ulp everywhere, exact on all but a few entries, and the relF gate."""
+    from test_oracle import bf16_ulp_distance
+    tr = os.path.join(GOLDEN, "torch_ref")
+    a = np.fromfile(os.path.join(tr, a_name), dtype=np.uint16).reshape(a_shape)
+    b = np.fromfile(os.path.join(tr, b_name), dtype=np.uint16).reshape(b_shape)
+    m, k = a_shape
+    n = b_shape[0]
+    g = np.fromfile(os.path.join(tr, gold), dtype=np.float32).reshape(m, n)
+    _log(f"[case] torch bf16 golden {gold} {preset}")
+    cfg = t0g.GemmConfig.preset(preset) if preset else None
+    c16 = run_gemm(rt, bufs, "NT", a, b, m, n, k, out=t0g.BF16, config=cfg)
+    d = bf16_ulp_distance(c16, o.f32_to_bf16_rne(g))
+    _log(f"[parity] {gold} {preset}: max {d.max()} bf16 ulp, {np.count_nonzero(d)} of {d.size} entries differ")
+    assert np.count_nonzero(d) <= 16
+    # Per entry: one bf16 ulp of the golden, plus what two fp32 sums of K terms in
+    # different orders may differ by (2 K 2^-24 sum|a b|).  Near-cancelled sums, whose bf16
+    # ulp is below that fp32 error, may differ by a few ulp; any real error exceeds it.
+    absab = o.gemm("NT", a & np.uint16(0x7FFF), b & np.uint16(0x7FFF), m, n, k)
+    tol = np.spacing(np.abs(g)) * 2.0 ** 16 + 2.0 * k * 2.0 ** -24 * absab
+    assert np.all(np.abs(o.bf16_to_f32(c16) - g) <= tol)
+    check_parity(o.bf16_to_f32(c16), g, k, f"bf16 out vs torch {gold} {preset}")
+    # precision_vs_torch.rs:302-303's own bound
+    assert np.abs(o.bf16_to_f32(c16) - g).max() < 0.05
+
+
 SUITE = [(128, 128, 128), (256, 256, 256), (128, 1024, 512), (256, 512, 128), (512, 512, 512),
          (1024, 1024, 1024), (33, 100, 50), (129, 65, 17), (100, 300, 200), (1000, 768, 512),
          (1, 1, 1), (7, 9, 3), (300, 8, 264), (64, 4096, 64)]
@@ -230,6 +266,33 @@ def test_c4a_thin(rt, bufs):
         a_st, b_st = stored_operands(layout, a_mk, b_nk)
         c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k)
         check_parity(c, ref, k, f"thin 128x4096x4096 {layout}")
+
+
+def uniform_half_bf16(n, seed):
+    """U(-0.5, 0.5) in bf16, two-sided as BASELINE's C4 configs state: the reference's
+    xorshift rand_bf16 (U(-1, 1), test_gemm_correctness.rs:45-58) halved, which is exact
+    in bf16.  The reference's own LCG (tile_boundary_tests.rs:42-49) only reaches [-0.5, 0)."""
+    return o.f32_to_bf16_rne(o.bf16_to_f32(o.rand_bf16_xorshift(n, seed)) * np.float32(0.5))
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(128, 4096, 4096, [0, 2, 4]), (256, 256, 32768, [0, 8, 16, 32])])
+def test_c4_two_sided_uniform(rt, bufs, m, n, k, splits):
+    """Both C4 shapes on two-sided U(-0.5, 0.5) data (sums that cancel, unlike the one-sided
+    LCG's): NT and NN, auto-selected and forced splits, fp32 and bf16 output."""
+    a_mk = uniform_half_bf16(m * k, 31 + m).reshape(m, k)
+    b_nk = uniform_half_bf16(n * k, 37 + n).reshape(n, k)
+    af = o.bf16_to_f32(a_mk)
+    assert af.min() < -0.4 and af.max() > 0.4 and abs(float(af.mean())) < 0.01
+    ref = o.gemm("NT", a_mk, b_nk, m, n, k)
+    for layout in ("NT", "NN"):
+        a_st, b_st = stored_operands(layout, a_mk, b_nk)
+        for sk in splits:
+            _log(f"[case] two-sided U(-0.5,0.5) {m}x{n}x{k} {layout} sk={sk}")
+            c = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, split_k=sk)
+            check_parity(c, ref, k, f"U(-0.5,0.5) {m}x{n}x{k} {layout} sk={sk}")
+            c16 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, split_k=sk, out=t0g.BF16)
+            assert np.array_equal(c16, o.f32_to_bf16_rne(c))
+            bufs.free()
 
 
 @pytest.mark.parametrize("split_k", [0, 8, 16, 32, 64])

@@ -76,6 +76,40 @@ def test_bf16_golden_is_rounded_fp32_result():
     assert np.all(np.abs(b16 - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-30)
 
 
+def bf16_ulp_distance(a16, b16):
+    """|a - b| in bf16 ulps (sign-magnitude bit patterns mapped onto one ordered integer line)."""
+    def line(b):
+        b = np.asarray(b).astype(np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    return np.abs(line(a16) - line(b16))
+
+
+# torch's bf16-output GEMMs (benchmarks/gen_torch_ref.py: torch.mm on bf16 operands, fp32
+# accumulation, bf16 result), the goldens src/t0/precision_vs_torch.rs:115-118 compares against
+BF16_GOLDENS = [("x.bin", (64, 256), "w_gate.bin", (512, 256), "h_gate_bf16acc.bin"),
+                ("x.bin", (64, 256), "w_up.bin", (512, 256), "h_up_bf16acc.bin"),
+                ("swiglu_bf16_trunc.bin", (64, 512), "w_down.bin", (256, 512), "y_bf16chain.bin")]
+
+
+@pytest.mark.parametrize("a_name,a_shape,b_name,b_shape,gold", BF16_GOLDENS)
+def test_bf16_output_mode_matches_torch_bf16_gemm(a_name, a_shape, b_name, b_shape, gold):
+    """The oracle's bf16 output (RNE of its fp32 result, t0g's bf16 mode) equals torch's bf16
+    GEMM to within one bf16 ulp everywhere, and exactly on all but a few entries (torch sums
+    in another order, so a result next to a rounding boundary may round the other way)."""
+    a = _bin(a_name, np.uint16, a_shape)
+    b = _bin(b_name, np.uint16, b_shape)
+    m, k = a_shape
+    n = b_shape[0]
+    g = _bin(gold, np.float32, (m, n))
+    assert np.array_equal(o.bf16_to_f32(o.f32_to_bf16_rne(g)), g)   # the golden is bf16-valued
+    got = o.f32_to_bf16_rne(o.gemm("NT", a, b, m, n, k))
+    d = bf16_ulp_distance(got, o.f32_to_bf16_rne(g))
+    assert d.max() <= 1 and np.count_nonzero(d) <= 8, (d.max(), np.count_nonzero(d))
+    # a truncating output (RTZ) or a wrong operand misses it by far more
+    trunc = o.f32_to_bf16_trunc(o.gemm("NT", a, b, m, n, k))
+    assert np.count_nonzero(bf16_ulp_distance(trunc, o.f32_to_bf16_rne(g))) > a_shape[0] * n // 10
+
+
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 @pytest.mark.parametrize("m,n,k", [(37, 23, 61), (64, 128, 300), (1, 5, 1), (16, 1, 7)])
 def test_fast_oracle_bit_equal_to_naive_loop(layout, m, n, k):
@@ -226,6 +260,21 @@ def test_parity_gate_subnormal_regime():
     dropped = mixed_ref.copy()
     dropped[0, :8] = 1e-35                              # ordinary values replaced by tiny ones
     assert not o.parity(dropped, mixed_ref, 256)[0]
+    # an output that is simply wrong over a reference made only of tiny values: relF has
+    # nothing to measure there, and max|d| = 1e-3 is inside the K-scaled bound
+    garbage = np.full_like(ref, 1e-3)
+    assert not o.parity(garbage, ref, 256)[0]
+    assert not o.parity(-flushed + 2.0 ** -80, ref, 256)[0]
+    # an entry of an ordinary matrix that cancels to exactly 0.0 in the CPU's sum keeps the
+    # GPU's fp32 summation noise, which is fine; an error there at the matrix's own scale is not
+    rng = np.random.default_rng(3)
+    dense = rng.standard_normal((64, 64)).astype(np.float32)
+    dense[5, 7] = 0.0
+    noisy = dense.copy()
+    noisy[5, 7] = 3e-8
+    assert o.parity(noisy, dense, 256)[0]
+    noisy[5, 7] = 0.008              # inside max|d|'s bound (0.01), not counted in relF
+    assert not o.parity(noisy, dense, 256)[0]
 
 
 def test_epilogue_chain_known_answers():

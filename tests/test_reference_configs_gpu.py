@@ -269,3 +269,41 @@ def test_ignis_forward_presets(rt, bufs, m, k, n):
     assert not np.any(got == SENTINEL)   # the whole padded tile grid is written, as the reference's kernel does
     ref = o.gemm("NT", xb.reshape(m, k), wtb, m, n, k)
     check_parity(got[:m, :n], ref, k, label)
+
+
+# examples/test_gemm_backward.rs:118-287: GemmConfig::tile_64x64_k16 for both gradients, its 7
+# sizes (M, K, N) and seeds; dX = dY * W through build_kernargs_backward_data on W = WT^T
+# (host transpose), dW = dY^T * X through build_kernargs_backward_weight on dY^T and X^T
+BACKWARD_SIZES = [(64, 64, 64), (128, 128, 128), (256, 256, 256), (128, 256, 512), (64, 512, 128), (256, 128, 256),
+                  (512, 256, 128)]
+
+
+@pytest.mark.parametrize("m,k,n", BACKWARD_SIZES)
+def test_gemm_backward_harness(rt, bufs, m, k, n):
+    cfg = t0g.GemmConfig.preset("tile_64x64_k16")
+    x = o.rand_bf16_xorshift(m * k, m * 100 + k)
+    w = o.rand_bf16_xorshift(n * k, n * 200 + k)          # WT [N][K]
+    dy = o.rand_bf16_xorshift(m * n, m * 300 + n)
+    kern = rt.ensure_gemm_kernel(cfg)
+    _log(f"[case] backward harness tile_64x64_k16 {m}x{k}x{n}")
+    # dX[M][K] = dY[M][N] * WT[N][K]
+    w_t = o.transpose_bf16(w, n, k)                        # W [K][N]
+    dya, wa = bufs.up(dy), bufs.up(w_t)
+    dx = bufs.up(np.full(m * k + 64, SENTINEL, dtype=np.float32))
+    ka = t0g.build_kernargs_backward_data(dya, wa, dx, m, n, k, cfg)
+    gx, gy = t0g.compute_grid_backward_data(cfg, m, k)
+    rt.dispatch(kern, [gx, gy, 1], ka)
+    got = rt.read(dx, (m * k + 64,), np.float32)
+    assert np.all(got[m * k:] == SENTINEL)
+    check_parity(got[:m * k].reshape(m, k), o.gemm("NN", dy, w, m, k, n), n, f"backward dX {m}x{k}x{n}")
+    # dW[N][K] = dY^T[N][M] * X[M][K]
+    dy_t = o.transpose_bf16(dy, m, n)                      # [N][M]
+    x_t = o.transpose_bf16(x, m, k)                        # [K][M]
+    dyta, xta = bufs.up(dy_t), bufs.up(x_t)
+    dw = bufs.up(np.full(n * k + 64, SENTINEL, dtype=np.float32))
+    ka = t0g.build_kernargs_backward_weight(dyta, xta, dw, m, n, k, cfg)
+    gx, gy = t0g.compute_grid_backward_weight(cfg, n, k)
+    rt.dispatch(kern, [gx, gy, 1], ka)
+    got = rt.read(dw, (n * k + 64,), np.float32)
+    assert np.all(got[n * k:] == SENTINEL)
+    check_parity(got[:n * k].reshape(n, k), o.gemm("TN", dy, x, n, k, m), m, f"backward dW {m}x{k}x{n}")

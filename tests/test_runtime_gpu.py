@@ -249,6 +249,36 @@ def test_stream_k_wait_that_gives_up_poisons_the_device():
         r.close()
 
 
+def test_stream_k_give_up_is_reported_after_a_stream_switch():
+    """As above, but the caller switches the handle to another stream right after the
+    stalled launch: the new stream is ordered after it, so its first wait still reads the
+    timeout count, returns T0G_ERR_TIMEOUT and poisons the device."""
+    from hip_rt import Stream
+    r = t0g.GpuRuntime.new(0)
+    side = Stream()
+    try:
+        m, n, k = 512, 512, 4096
+        a = r.upload(o.rand_bf16_xorshift(m * k, 5))
+        b = r.upload(o.rand_bf16_xorshift(k * n, 6))
+        c = r.alloc(m * n * 4)
+        sk = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
+        t0g.set_stream_k_spin_limit(64)
+        t0g.debug_stream_k_stall(True)
+        try:
+            r.gemm(a, b, c, m, n, k, transpose="NN", config=sk)
+            r.set_stream(side.ptr)
+            with pytest.raises(t0g.T0gError) as e:
+                r.wait_idle()
+            assert e.value.code == t0g.ERR_TIMEOUT and "stream-K" in str(e.value)
+        finally:
+            t0g.debug_stream_k_stall(False)
+            t0g.set_stream_k_spin_limit(1 << 20)
+        assert r.is_poisoned()
+    finally:
+        r.close()
+        side.destroy()
+
+
 # ---- grouped GEMMs keep each stream's workspace ------------------------------------
 
 def test_gemm_group_workspace_growth_on_the_device_stream():

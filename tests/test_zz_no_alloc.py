@@ -182,3 +182,126 @@ def test_noalloc_refuses_more_scratch_than_it_has(rt):
         gemm_noalloc(rt, d)
     assert e.value.code == t0g.ERR_INVALID_ARG and "scratch" in str(e.value)
     assert not rt.is_poisoned()
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_on_a_fresh_handle_allocates_nothing():
+    """The property the entry point exists for.  On a handle that has launched nothing
+    (no split-K workspace, no control block, no kernel looked up yet) the first call, a
+    split-K plan whose planes go to the scratch, makes no device allocation: the library's
+    count of hipMalloc calls and code-object loads does not move.  The same holds with the
+    timeline diagnostic switched on (its instrumented code object is never loaded here).
+    t0g_gemm on the same handle does allocate (its workspace), which shows the count sees it."""
+    m, n, k = 128, 4096, 4096
+    a = o.rand_bf16_lcg(m * k, 61)
+    b = o.rand_bf16_lcg(n * k, 62)
+    ref = o.gemm("NT", a, b, m, n, k)
+    fresh = t0g.GpuRuntime.new(0)
+    try:
+        da, db, c = fresh.upload(a), fresh.upload(b), fresh.alloc(m * n * 4)
+        desc = t0g.gemm_desc(da, db, c, m, n, k, split_k=2)
+        assert t0g.gemm_workspace_size(desc) == 2 * m * n * 4          # a split plan: planes in the scratch
+        before = t0g.device_alloc_count()
+        fresh.gemm_noalloc(desc)
+        fresh.wait_idle()
+        assert t0g.device_alloc_count() == before, "t0g_gemm_noalloc allocated device memory"
+        ok, relf, maxabs, _ = o.parity(fresh.read(c, (m, n), np.float32), ref, k)
+        assert ok, (relf, maxabs)
+        t0g.set_timeline(1)
+        try:
+            fresh.memset(c, 0, m * n * 4)
+            before = t0g.device_alloc_count()
+            fresh.gemm_noalloc(desc)
+            fresh.wait_idle()
+            assert t0g.device_alloc_count() == before, "the timeline build was loaded"
+        finally:
+            t0g.set_timeline(0)
+        assert o.parity(fresh.read(c, (m, n), np.float32), ref, k)[0]
+        before = t0g.device_alloc_count()
+        fresh.gemm_desc(desc)                       # t0g_gemm: its workspace is a hipMalloc
+        fresh.wait_idle()
+        assert t0g.device_alloc_count() > before
+        for x in (da, db, c):
+            fresh.free(x)
+    finally:
+        fresh.close()
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_from_two_handles_take_the_scratch_in_turn():
+    """Two handles (two streams) on one GPU, each enqueueing split-K calls into the shared
+    scratch with no wait in between: each call waits for the previous user's event, so
+    every result equals the same problem run alone through t0g_gemm."""
+    h1, h2 = t0g.GpuRuntime.new(0), t0g.GpuRuntime.new(0)
+    bufs = []
+    try:
+        probs = []
+        for i, (h, (m, n, k)) in enumerate([(h1, (256, 2048, 8192)), (h2, (512, 1024, 4096)),
+                                             (h1, (128, 4096, 4096)), (h2, (256, 256, 32768))]):
+            a = o.rand_bf16_lcg(m * k, 70 + i)
+            b = o.rand_bf16_lcg(n * k, 80 + i)
+            da, db, c = h.upload(a), h.upload(b), h.alloc(m * n * 4)
+            bufs.append((h, (da, db, c)))
+            d = t0g.gemm_desc(da, db, c, m, n, k, split_k=8)
+            assert t0g.gemm_workspace_size(d) > 0
+            probs.append((h, d, a, b, c, m, n, k))
+        for h, d, *_ in probs:                      # enqueued back to back on two streams
+            h.gemm_noalloc(d)
+        h1.wait_idle()
+        h2.wait_idle()
+        for h, d, a, b, c, m, n, k in probs:
+            got = h.read(c, (m, n), np.float32)
+            h.memset(c, 0, m * n * 4)
+            h.gemm_desc(d)                          # alone, library workspace
+            h.wait_idle()
+            assert np.array_equal(got, h.read(c, (m, n), np.float32)), f"{m}x{n}x{k}"
+            assert o.parity(got, o.gemm("NT", a, b, m, n, k), k)[0]
+    finally:
+        for h, xs in bufs:
+            for x in xs:
+                h.free(x)
+        h1.close()
+        h2.close()
+
+
+@pytest.mark.gpu
+def test_noalloc_under_hip_graph_capture():
+    """A split-K call captured into a HIP graph on a caller stream and replayed: every
+    replay, with eager work and synchronisations in between, equals the eager call bit
+    for bit, and replaying allocates nothing."""
+    from hip_rt import Graph, Stream
+    m, n, k = 256, 1024, 8192
+    a = o.rand_bf16_lcg(m * k, 91)
+    b = o.rand_bf16_lcg(n * k, 92)
+    h = t0g.GpuRuntime.new(0)
+    s = Stream()
+    g = None
+    try:
+        da, db = h.upload(a), h.upload(b)
+        c_eager, c_graph, c_other = h.alloc(m * n * 4), h.alloc(m * n * 4), h.alloc(m * n * 4)
+        d_eager = t0g.gemm_desc(da, db, c_eager, m, n, k, split_k=4)
+        d_graph = t0g.gemm_desc(da, db, c_graph, m, n, k, split_k=4)
+        h.gemm_noalloc(d_eager)
+        h.wait_idle()
+        want = h.read(c_eager, (m, n), np.float32)
+        assert o.parity(want, o.gemm("NT", a, b, m, n, k), k)[0]
+        h.set_stream(s.ptr)
+        g = Graph(s, lambda: h.gemm_noalloc(d_graph))
+        before = t0g.device_alloc_count()
+        for rep in range(3):
+            h.memset(c_graph, 0, m * n * 4)
+            g.launch(s)
+            s.synchronize()
+            got = h.read(c_graph, (m, n), np.float32)
+            assert np.array_equal(got, want), f"replay {rep}"
+            h.gemm_noalloc(t0g.gemm_desc(db, da, c_other, 256, 256, 1024, split_k=2))   # eager work between
+            h.wait_idle()
+        assert t0g.device_alloc_count() == before
+        h.set_stream(None)
+        for x in (da, db, c_eager, c_graph, c_other):
+            h.free(x)
+    finally:
+        if g is not None:
+            g.destroy()
+        h.close()
+        s.destroy()
