@@ -502,6 +502,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the other benchmark configurations")
     ap.add_argument("--no-clock", action="store_true", help="skip the shader-clock sampling (amd-smi) lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--clock", action="store_true",
+                    help="with --only LAYOUT:M:N:K: also sample the shader clock and socket power (amd-smi) "
+                         "while that GEMM runs back to back, and the MFMA utilisation they imply")
     ap.add_argument("--timeline", action="store_true",
                     help="with --only LAYOUT:M:N:K: also record one launch's per-workgroup timeline (entry, end "
                          "of the K loop, stores done; t0g_set_timeline) and print its per-XCD summary")
@@ -595,6 +598,10 @@ def main():
                 "tflops": round(r["flop"] / sec / 1e12, 2),
                 "frac_of_peak": round(r["flop"] / sec / 1e12 / PEAK_TFLOPS, 4),
                 "gbs_min_bytes": round(r["bytes_min"] / sec / 1e9, 1)}
+        if args.clock:
+            ck = clock_line(torch, rt, r["desc"], r["flop"], seconds=3.0)
+            ck.update(_mfma_util(r["flop"] / sec / 1e12, ck.get("sclk_mhz_median")))
+            line["clock"] = ck
         if args.timeline:
             line["timeline"] = timeline_summary(t0g, torch, rt, r["desc"], k)
         print(json.dumps(line), flush=True)
