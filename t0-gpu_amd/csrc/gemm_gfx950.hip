@@ -647,28 +647,60 @@ __device__ __forceinline__ u32x4_t rsrc_words(uint64_t base, uint32_t bytes, uin
     return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
 }
 
-// rsrc_words for shifts below 2^32 (the operands of the non-wide kernels), in
-// 32-bit scalar arithmetic: the 64-bit compare of rsrc_words has no scalar
-// instruction and costs vector ones.  The words are uniform; readfirstlane
-// states it so they stay in scalar registers.
+// Descriptors read by the LDS-DMA asm are formed in scalar instructions only.
+// A VALU write of an SGPR (v_readfirstlane, the form the compiler picks for a
+// saturating subtract) needs wait states before a VMEM instruction reads that
+// SGPR, and the compiler does not see the reads inside the asm: placed right
+// before the first request of a group, it gave wrong results.  SALU writes
+// need none (a VALU write read by SALU is interlocked).  The inputs are
+// uniform: readfirstlane moves any the compiler holds in VGPRs to SGPRs.
 __device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+// {base + shift (48-bit address, high word masked), rec, word 3}
+__device__ __forceinline__ u32x4_t rsrc_scalar(uint64_t base, uint64_t shift, uint32_t rec) {
+    uint32_t lo, hi;
+    asm("s_add_u32 %0, %2, %4\n\t"
+        "s_addc_u32 %1, %3, %5\n\t"
+        "s_and_b32 %1, %1, 0xffff"
+        : "=&s"(lo), "=&s"(hi)
+        : "s"(uniform_u32((uint32_t)base)), "s"(uniform_u32((uint32_t)(base >> 32))),
+          "s"(uniform_u32((uint32_t)shift)), "s"(uniform_u32((uint32_t)(shift >> 32)))
+        : "scc");
+    return u32x4_t{lo, hi, rec, (uint32_t)kRsrcWord3};
+}
+
+// rsrc_words for shifts below 2^32 (the operands of the non-wide kernels):
+// rec = max(bytes - shift, 0) by s_sub_u32 (SCC = borrow) and s_cselect.
 __device__ __forceinline__ u32x4_t rsrc_words32(uint64_t base, uint32_t bytes, uint32_t shift) {
-    const uint32_t rec = shift < bytes ? bytes - shift : 0u;
-    const uint64_t a = base + shift;
-    return u32x4_t{uniform_u32((uint32_t)a), uniform_u32((uint32_t)(a >> 32) & 0xFFFFu), uniform_u32(rec),
-                   (uint32_t)kRsrcWord3};
+    uint32_t rec;
+    asm("s_sub_u32 %0, %1, %2\n\t"
+        "s_cselect_b32 %0, 0, %0"
+        : "=&s"(rec)
+        : "s"(uniform_u32(bytes)), "s"(uniform_u32(shift))
+        : "scc");
+    return rsrc_scalar(base, shift, rec);
 }
 
 // Wide form of rsrc_words for operands of any size: [base + shift, base + bytes)
 // cut to its first 2 GiB (kOob stays out of range).  Callers shift it to the
 // tile's first row (K-contiguous operands) or the stage's first k row
 // (M/N-contiguous operands), so that every offset they use from there is below
-// 2 GiB; the host checks the leading dimensions for that.
+// 2 GiB; the host checks the leading dimensions for that.  rec = min(max(bytes
+// - shift, 0), kOob) in 64-bit scalar arithmetic.
 __device__ __forceinline__ u32x4_t rsrc_words_wide(uint64_t base, uint64_t bytes, uint64_t shift) {
-    const uint64_t left = shift < bytes ? bytes - shift : 0u;
-    const uint32_t rec = left < (uint64_t)kOob ? (uint32_t)left : kOob;
-    const uint64_t a = base + shift;
-    return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, rec, (uint32_t)kRsrcWord3};
+    uint32_t lo, hi;
+    asm("s_sub_u32 %0, %2, %4\n\t"
+        "s_subb_u32 %1, %3, %5\n\t"
+        "s_cselect_b32 %0, 0, %0\n\t"       // borrow out: shift > bytes
+        "s_cselect_b32 %1, 0, %1\n\t"
+        "s_cmp_lg_u32 %1, 0\n\t"
+        "s_cselect_b32 %0, 0x80000000, %0\n\t"
+        "s_min_u32 %0, %0, 0x80000000"
+        : "=&s"(lo), "=&s"(hi)
+        : "s"(uniform_u32((uint32_t)bytes)), "s"(uniform_u32((uint32_t)(bytes >> 32))),
+          "s"(uniform_u32((uint32_t)shift)), "s"(uniform_u32((uint32_t)(shift >> 32)))
+        : "scc");
+    static_assert(kOob == 0x80000000u, "the asm clamps to kOob");
+    return rsrc_scalar(base, shift, lo);
 }
 
 // Bytes spanned by an operand of `rows` M/N rows and k K values with leading
@@ -690,6 +722,36 @@ __device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voff, uint32_t lds_
         :
         : "v"(voff), "s"(rsrc), "s"(lds_m0)
         : "memory", "m0");
+}
+
+// Grouped LDS DMA: the instruction's 12-bit immediate offset is added to both
+// the descriptor offset and the LDS address (M0 + OFF + 16 * lane), so up to
+// four 1 KB requests into consecutive LDS kilobytes share one M0 write: the
+// group sets M0 once (dma_m0, with the wait state an SALU write of M0 needs
+// before an LDS-DMA instruction reads it) and each request passes its piece's
+// byte offset less OFF.  M0 is not otherwise used by this code (LDS
+// instructions on gfx950 do not read it), so it holds between the requests.
+__device__ __forceinline__ void dma_m0(uint32_t lds_base, uint32_t lds_off) {
+    asm volatile(
+        "s_add_u32 m0, %0, %1\n\t"
+        "s_nop 0"
+        :
+        : "s"(lds_base), "s"(lds_off)
+        : "memory", "m0", "scc");
+}
+template <uint32_t OFF>
+__device__ __forceinline__ void dma16_off(u32x4_t rsrc, uint32_t voff) {
+    static_assert(OFF < 4096, "12-bit immediate offset");
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen offset:%2 lds" : : "v"(voff), "s"(rsrc), "i"(OFF) : "memory");
+}
+// Request `slot` (0..3) of a group set up by dma_m0.
+__device__ __forceinline__ void dma16_slot(u32x4_t rsrc, uint32_t voff, int slot) {
+    switch (slot) {
+        case 0: dma16_off<0>(rsrc, voff); break;
+        case 1: dma16_off<1024>(rsrc, voff); break;
+        case 2: dma16_off<2048>(rsrc, voff); break;
+        default: dma16_off<3072>(rsrc, voff); break;
+    }
 }
 
 // dma16 with the LDS address formed as lds_base + lds_off by one scalar add

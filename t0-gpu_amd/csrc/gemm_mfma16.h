@@ -35,11 +35,14 @@ template <bool K_MAJOR, int ROWS, int NT, int SUBS, bool WIDE = false>
 struct Op16;
 
 // K-contiguous operand of a 256-row tile, 64 K values per stage: 128-byte LDS
-// rows, chunk swizzle fk<64>.  DMA instruction i of a wave covers rows
-// 8 (i W + wave) + lane / 8 (W waves); for even W, fk<64> of those rows does not
-// depend on i, so one K column serves all of a wave's instructions, and their
-// byte offsets are kept in registers (the stage's K position is in the
-// descriptor's base).
+// rows, chunk swizzle fk<64>.  A stage is 32 pieces of 1 KB, piece q = rows
+// 8q .. 8q+7 at LDS offset q KB.  Whole stages: wave w issues pieces
+// w kInstr + i, in groups of four consecutive pieces sharing one M0 write
+// (dma_m0); the lanes' byte offsets, less the requests' immediate offsets, are
+// kept in registers (the stage's K position is in the descriptor's base).
+// Stages with a K tail (CHECK): wave w issues pieces i W + w, one M0 write
+// each; for even W, fk<64> of those rows does not depend on i, so one K column
+// serves all of a wave's instructions.
 template <int ROWS, int NT, int SUBS, bool WIDE>
 struct Op16<true, ROWS, NT, SUBS, WIDE> {
     typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
@@ -54,7 +57,10 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
     uint32_t step;    // bytes between instructions (8 W rows)
     uint32_t wave;
     uint32_t frag[2];   // per 32-wide K step: LDS offset of the lane's chunk in sub-tile 0
-    uint32_t offs[kInstr];   // off0 + i * step: whole stages issue their DMA with no address arithmetic
+    // whole stages: byte offset of piece wave * kInstr + i, less (i % 4) KB (the
+    // request's immediate offset).  Not negative: the piece's rows start at
+    // 8 i, i.e. 16 i ld >= 1 KB * i bytes in, since ld >= K >= 64 here.
+    uint32_t offs[kInstr];
 
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -71,7 +77,12 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         }
         step = 16 * kWaves * ld;
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) offs[i] = off0 + i * step;
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t rq = 8 * (wave * kInstr + i) + (lane >> 3);
+            const uint32_t cq = (lane & 7u) ^ fk<64>(rq);
+            const uint32_t o = WIDE ? (rq * ld + cq * 8) * 2 : ((row0 + rq) * ld + cq * 8) * 2;
+            offs[i] = o - (uint32_t)(i & 3) * 1024u;
+        }
         const uint32_t row = wrow + (lane & 15u), qk = lane >> 4;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) frag[kk] = row * kKRow + (((4u * kk + qk) ^ fk<64>(row)) << 4);
@@ -82,13 +93,15 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
         else
             return rsrc_words32(base, bytes, k0 * 2);
     }
+    // Requests of a stage go out in ascending i (the group's M0 is written at i % 4 == 0).
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
-        const uint32_t m0 = lds + (i * kWaves + wave) * 1024;
-        if (CHECK)
-            dma16(r, k0 + kcol < kend ? off0 + i * step : kOob, m0);
-        else
-            dma16_at(r, offs[i], lds + wave * 1024, i * kWaves * 1024);
+        if (CHECK) {
+            dma16(r, k0 + kcol < kend ? off0 + i * step : kOob, lds + (i * kWaves + wave) * 1024);
+        } else {
+            if ((i & 3) == 0) dma_m0(lds, (wave * kInstr + i) * 1024);
+            dma16_slot(r, offs[i], i & 3);
+        }
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,
@@ -110,10 +123,15 @@ struct Op16<true, ROWS, NT, SUBS, WIDE> {
 };
 
 // M/N-contiguous operand of a 256-column tile: LDS rows are k rows of 512
-// bytes, granule swizzle fm16.  DMA instruction i of a wave covers k rows
-// 2 (i W + wave) + lane / 32 (W waves); their swizzle depends on i only through
+// bytes, granule swizzle fm16.  A stage is 32 pieces of 1 KB, piece q = k rows
+// 2q, 2q+1 at LDS offset q KB.  Whole stages: wave w issues pieces
+// w kInstr + i in groups of four sharing one M0 write, from byte offsets kept
+// in registers less the requests' immediate offsets (not negative for
+// ld >= 256: the piece starts 2 i k rows in; the host keeps smaller leading
+// dimensions off these kernels).  Stages with a K tail (CHECK): wave w issues
+// pieces i W + w, one M0 write each; their swizzle depends on i only through
 // bit 0 of i (W = 4) or not at all (W = 8), so every instruction's byte offset
-// is one of two bases plus i steps, kept in registers.
+// is one of two bases plus i steps.
 template <int ROWS, int NT, int SUBS, bool WIDE>
 struct Op16<false, ROWS, NT, SUBS, WIDE> {
     typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type bytes_t;
@@ -129,7 +147,7 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
     uint32_t step;     // bytes between instructions (2 W k rows)
     uint32_t wave;
     uint32_t frag0;    // K step 0, half 0, sub-tile 0; sub-tile s is frag0 ^ (s << 5)
-    uint32_t offs[kInstr];   // off[i & 1] + i * step: whole stages issue their DMA with no address arithmetic
+    uint32_t offs[kInstr];   // whole stages: piece wave * kInstr + i, less (i % 4) KB
 
     __device__ __forceinline__ void init(uint32_t tid, uint32_t row0, uint32_t ld, uint32_t wrow) {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -143,7 +161,11 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
             off[i] = (k * ld + row0 + lg * 16 + (slot & 1) * 8) * 2;
         }
 #pragma unroll
-        for (int i = 0; i < kInstr; ++i) offs[i] = off[i & 1] + i * step;
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t kq = 2 * (wave * kInstr + i) + (lane >> 5);
+            const uint32_t lg = (slot >> 1) ^ fm16(kq, kGranules);
+            offs[i] = (kq * ld + row0 + lg * 16 + (slot & 1) * 8) * 2 - (uint32_t)(i & 3) * 1024u;
+        }
         // ds_read_b64_tr_b16: 16-lane group q reads k rows 32*kk + 8q + 4h + r
         // (lane 4r + c: columns 4c .. 4c+3 of the 16-column sub-tile); lane i
         // of the group receives column i.  fm16 sees only k % 4 and bit 3 of k.
@@ -159,13 +181,16 @@ struct Op16<false, ROWS, NT, SUBS, WIDE> {
         else
             return rsrc_words32(base, bytes, k0 * ld * 2);
     }
+    // Requests of a stage go out in ascending i (the group's M0 is written at i % 4 == 0).
     template <bool CHECK>
     __device__ __forceinline__ void issue_one(int i, u32x4_t r, uint32_t lds, uint32_t k0, uint32_t kend) const {
-        const uint32_t m0 = lds + (i * kWaves + wave) * 1024;
-        if (CHECK)
-            dma16(r, k0 + krow + 2 * kWaves * i < kend ? off[i & 1] + i * step : kOob, m0);
-        else
-            dma16_at(r, offs[i], lds + wave * 1024, i * kWaves * 1024);
+        if (CHECK) {
+            dma16(r, k0 + krow + 2 * kWaves * i < kend ? off[i & 1] + i * step : kOob,
+                  lds + (i * kWaves + wave) * 1024);
+        } else {
+            if ((i & 3) == 0) dma_m0(lds, (wave * kInstr + i) * 1024);
+            dma16_slot(r, offs[i], i & 3);
+        }
     }
     template <bool CHECK>
     __device__ __forceinline__ void issue(uint32_t lds, uint64_t base, bytes_t bytes, uint32_t ld, uint32_t k0,

@@ -319,6 +319,17 @@ enum class OperandPath { Fast, Wide, Elementwise };
 constexpr uint32_t kMaxKMajorLd = 1u << 22;
 constexpr uint32_t kMaxMnMajorLd = (1u << 24) - 256;
 
+// The 256x256 kernels issue a stage's DMA in groups of four 1 KB requests
+// sharing one M0 value; each request's offset register holds its piece's byte
+// offset less up to 3 KB (the instruction's immediate offset adds it back).  An
+// M/N-contiguous operand's piece i of wave 0 starts 2 i k rows, i.e. 4 i ld
+// bytes, in: not below i KB only for ld >= 256.  Smaller leading dimensions of
+// M/N-contiguous operands therefore stay off those kernels (a K-contiguous
+// operand on a whole-stage loop has ld >= K >= 64, which is enough there).
+static bool ld_fits_256(uint32_t t, uint32_t lda, uint32_t ldb) {
+    return (a_k_major(t) || lda >= 256) && (b_k_major(t) || ldb >= 256);
+}
+
 static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, uint32_t k, uint32_t lda,
                                 uint32_t ldb, uint32_t t) {
     if ((a & 15) || (b & 15) || (lda & 7) || (ldb & 7)) return OperandPath::Elementwise;
@@ -327,7 +338,8 @@ static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, 
     const uint64_t a_elems = a_k_major(t) ? (uint64_t)m * lda : (uint64_t)k * lda;
     const uint64_t b_elems = b_k_major(t) ? (uint64_t)n * ldb : (uint64_t)k * ldb;
     if (a_elems < (1ull << 30) && b_elems < (1ull << 30)) return OperandPath::Fast;
-    if (lda < (a_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd) && ldb < (b_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd))
+    if (lda < (a_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd) && ldb < (b_k_major(t) ? kMaxKMajorLd : kMaxMnMajorLd) &&
+        ld_fits_256(t, lda, ldb))
         return OperandPath::Wide;
     return OperandPath::Elementwise;
 }
@@ -338,13 +350,15 @@ static OperandPath operand_path(uint64_t a, uint64_t b, uint32_t m, uint32_t n, 
 // caller guarantees the division and a multiple of 8 per slice: the fp32
 // planes are the caller's, with the reference's partition); otherwise slices
 // are rounded to whole 64-K stages and the split may shrink.
-static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, OperandPath path, uint32_t m,
-                     uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p, bool allow_fused = false,
+// fits_256: ld_fits_256() of the operands.
+static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, OperandPath path, bool fits_256,
+                     uint32_t m, uint32_t n, uint32_t k, uint32_t split_req, GemmPlan *p, bool allow_fused = false,
                      bool exact_split = false) {
     const bool aligned = path != OperandPath::Elementwise, wide = path == OperandPath::Wide;
     bool stream_k = split_req == T0G_STREAM_K;
     if (stream_k) split_req = 1;
     if (!aligned && tile->bm == 256) tile = &kTiles[1];   // no element-wise-load variant of the 256x256 tile
+    if (!fits_256 && tile->bm == 256) tile = &kTiles[1];
     if (wide) tile = &kTiles[0];                           // the wide kernels are 256x256 only
     if (tile->bm != 256 || k == 0 || wide) stream_k = false;   // the data-parallel kernel then
     p->stream_k = stream_k;
@@ -626,7 +640,8 @@ static int resolve_desc(const t0g_gemm_desc *d, t0g_gemm_config *cfg, GemmPlan *
         if ((rc = check_extent("A", a_k_major(t) ? d->m : d->k, o->lda))) return rc;
         if ((rc = check_extent("B", b_k_major(t) ? d->n : d->k, o->ldb))) return rc;
     }
-    return make_plan(tile, t, d->out_dtype == T0G_BF16, path, d->m, d->n, d->k, sk, plan, allow_fused);
+    return make_plan(tile, t, d->out_dtype == T0G_BF16, path, ld_fits_256(t, o->lda, o->ldb), d->m, d->n, d->k, sk,
+                     plan, allow_fused);
 }
 
 // Device workspace a plan needs: stream-K partial slots, fused split-K tile
@@ -1190,7 +1205,9 @@ static int dispatch_ref(t0g_device *dev, const t0g_kernel *kn, uint32_t tiles_m,
             if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
         }
         GemmPlan p;
-        if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p, false, true))) return rc;
+        if ((rc = make_plan(tile, cfg.transpose, false, path, ld_fits_256(cfg.transpose, o.lda, o.ldb), o.m, o.n, o.k,
+                            sk, &p, false, true)))
+            return rc;
         o.c_split_stride = y_split_stride;
         return run_plan(dev, p, o, 0);
     }
@@ -1297,7 +1314,9 @@ static int dispatch_gemm(t0g_device *dev, const t0g_kernel *kn, const uint32_t g
         if ((rc = check_extent("WT", cfg.transpose == T0G_NN ? o.k : o.n, o.ldb))) return rc;
     }
     GemmPlan p;
-    if ((rc = make_plan(tile, cfg.transpose, false, path, o.m, o.n, o.k, sk, &p, lib_planes))) return rc;
+    if ((rc = make_plan(tile, cfg.transpose, false, path, ld_fits_256(cfg.transpose, o.lda, o.ldb), o.m, o.n, o.k, sk,
+                        &p, lib_planes)))
+        return rc;
     if (p.tile != tile)   // another tile than the caller's grid was built for: refuse rather than re-grid
         return fail(T0G_ERR_UNSUPPORTED_CONFIG,
                     "tile %ux%u cannot take these operands (rows must be 16-byte aligned with K %% 8 == 0; "

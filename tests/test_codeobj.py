@@ -162,6 +162,22 @@ def test_compile_split_k_writes_planes_to_c():
     assert e.value.code == t0g.ERR_UNSUPPORTED_CONFIG
 
 
+@pytest.mark.parametrize("layout,m,n,lda,ldb,tile", [
+    ("NN", 384, 200, 0, 248, 128), ("NN", 384, 248, 0, 256, 256), ("NN", 4096, 4096, 0, 0, 256),
+    ("TN", 200, 200, 248, 248, 128), ("TN", 256, 256, 256, 256, 256), ("TN", 248, 512, 248, 512, 128),
+    ("TT", 200, 320, 200, 0, 128), ("TT", 256, 320, 264, 0, 256),
+    ("NT", 200, 200, 0, 0, 256)])
+def test_small_mn_contiguous_ld_stays_off_the_256_kernels(layout, m, n, lda, ldb, tile):
+    """The 256x256 kernels' grouped LDS DMA needs ld >= 256 for M/N-contiguous
+    operands (offset registers hold a piece's offset less up to 3 KB); K-contiguous
+    operands are unaffected.  The 256x256 preset with a smaller such ld runs on the
+    128x128 kernels, with stream-K asked for too."""
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64")
+    for c in (cfg, cfg.copy(split_k=t0g.STREAM_K)):
+        d = t0g.gemm_desc(1 << 20, 1 << 26, 1 << 30, m, n, 512, transpose=layout, lda=lda, ldb=ldb, config=c)
+        assert t0g.gemm_kernel_name(d).startswith(f"t0g_gemm_{tile}x{tile}_k64_{layout.lower()}_")
+
+
 def test_compile_stream_k_falls_back_to_the_same_tile():
     cfg = t0g.GemmConfig.preset("gfx950_256x256_k64").copy(split_k=t0g.STREAM_K)
     ck = t0g.gemm_compile(t0g.gemm_desc(1 << 20, 1 << 26, 1 << 30, 4352, 8192, 4096, transpose="NN", config=cfg))

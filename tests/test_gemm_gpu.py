@@ -99,6 +99,43 @@ def check_parity(c_gpu, c_ref, k, label):
 PRESETS = ["gfx950_256x256_k64", "gfx950_128x128_k64", "gfx950_64x64_k64"]
 
 
+def _padded(arr, ld, fill):
+    """arr [rows][cols] stored with row pitch ld >= cols; the padding holds `fill`."""
+    out = np.full((arr.shape[0], ld), fill, dtype=arr.dtype)
+    out[:, :arr.shape[1]] = arr
+    return out
+
+
+@pytest.mark.parametrize("layout", ["NN", "TN", "TT"])
+@pytest.mark.parametrize("dim,ld", [(200, 200), (200, 248), (248, 256), (256, 256), (256, 264), (512, 512)])
+def test_mn_contiguous_leading_dimension_around_256(rt, bufs, layout, dim, ld):
+    """The 256x256 kernels issue each stage's LDS DMA in groups of four requests
+    sharing one M0 value, which needs ld >= 256 for an M/N-contiguous operand; the
+    host runs smaller leading dimensions on the 128x128 kernels.  Both sides of that
+    boundary, with the 256x256 preset asked for: the M/N-contiguous operand(s) have
+    `dim` rows/columns stored with pitch `ld`, padding filled with 1e4 (a read of it
+    into a valid output would fail the gate)."""
+    k = 512
+    m = dim if layout in ("TN", "TT") else 384
+    n = dim if layout in ("NN", "TN") else 320
+    _log(f"[case] mn-ld layout={layout} m={m} n={n} k={k} ld={ld}")
+    a_mk = o.rand_bf16_xorshift(m * k, 11 + dim).reshape(m, k)
+    b_nk = o.rand_bf16_xorshift(n * k, 29 + ld).reshape(n, k)
+    ref = o.gemm_nt_naive(a_mk, b_nk, m, k, n)
+    a_st, b_st = stored_operands(layout, a_mk, b_nk)
+    big = o.f32_to_bf16_rne(np.full(1, 1.0e4, dtype=np.float32))[0]
+    lda = ldb = 0
+    if layout in ("TN", "TT"):
+        a_st, lda = _padded(a_st, ld, big), ld
+    if layout in ("NN", "TN"):
+        b_st, ldb = _padded(b_st, ld, big), ld
+    cfg = t0g.GemmConfig.preset("gfx950_256x256_k64")
+    d = t0g.gemm_desc(1 << 20, 1 << 26, 1 << 30, m, n, k, transpose=layout, lda=lda, ldb=ldb, config=cfg)
+    assert t0g.gemm_kernel_name(d).startswith("t0g_gemm_256x256" if ld >= 256 else "t0g_gemm_128x128")
+    c32 = run_gemm(rt, bufs, layout, a_st, b_st, m, n, k, config=cfg, lda=lda, ldb=ldb)
+    check_parity(c32, ref, k, f"mn-ld {layout} dim={dim} ld={ld}")
+
+
 @pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 @pytest.mark.parametrize("preset", PRESETS + [None])
 def test_c1_256_cubed_all_layouts(rt, bufs, layout, preset):
