@@ -1469,24 +1469,45 @@ __device__ __forceinline__ uint32_t bf16_bits_ref(float x) {
 }
 }  // namespace t0g
 
+// Vector form: each wave converts 128 items of 4 elements per grid step with
+// two 16-byte non-temporal loads per lane, each instruction covering 1 KB of
+// consecutive items (whole lines), and two 8-byte stores (512 consecutive bytes
+// per instruction).  The host launches one step for every wave up to 2^20
+// workgroups.  Measured against 8 elements per lane from 32 contiguous bytes in
+// a grid of 8192 workgroups: 64 Mi elements in 58.4 against 66.6 us; a full grid
+// of that form took 62.4 us, and more loads in flight per lane were slower.
+// Whole waves run without per-lane bounds tests (those cost 61.2 us).
 extern "C" __global__ void __launch_bounds__(256) t0g_f32_to_bf16_rne(T0gConvertArgs p) {
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
-    const uint64_t stride = (uint64_t)p.grid_blocks * 256;
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) f32x4_t gf32x4_t;
+    typedef __attribute__((address_space(1))) u32x2_t gu32x2_t;
     if (p.flags & T0G_CONVERT_VEC) {
-        const uint64_t n8 = p.n >> 3;
-        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
-            const __attribute__((address_space(1))) f32x4_t* s =
-                reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>((uintptr_t)p.src) + 2 * i;
-            const f32x4_t lo = __builtin_nontemporal_load(s), hi = __builtin_nontemporal_load(s + 1);
-            u32x4_t w;
-            w[0] = t0g::bf16_bits_ref(lo[0]) | (t0g::bf16_bits_ref(lo[1]) << 16);
-            w[1] = t0g::bf16_bits_ref(lo[2]) | (t0g::bf16_bits_ref(lo[3]) << 16);
-            w[2] = t0g::bf16_bits_ref(hi[0]) | (t0g::bf16_bits_ref(hi[1]) << 16);
-            w[3] = t0g::bf16_bits_ref(hi[2]) | (t0g::bf16_bits_ref(hi[3]) << 16);
-            reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)p.dst)[i] = w;
+        const uint64_t n4 = p.n >> 2;   // items of 4 elements
+        const uint32_t lane = threadIdx.x & 63u;
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const uint64_t step = (uint64_t)p.grid_blocks * 4 * 128;
+        gf32x4_t* const s = reinterpret_cast<gf32x4_t*>((uintptr_t)p.src);
+        gu32x2_t* const d = reinterpret_cast<gu32x2_t*>((uintptr_t)p.dst);
+        auto pack4 = [](f32x4_t v) {
+            return u32x2_t{t0g::bf16_bits_ref(v[0]) | (t0g::bf16_bits_ref(v[1]) << 16),
+                           t0g::bf16_bits_ref(v[2]) | (t0g::bf16_bits_ref(v[3]) << 16)};
+        };
+        for (uint64_t wb = ((uint64_t)blockIdx.x * 4 + wave) * 128; wb < n4; wb += step) {
+            if (wb + 128 <= n4) {
+                const f32x4_t a = __builtin_nontemporal_load(s + wb + lane);
+                const f32x4_t b = __builtin_nontemporal_load(s + wb + 64 + lane);
+                d[wb + lane] = pack4(a);
+                d[wb + 64 + lane] = pack4(b);
+            } else {
+                const uint64_t i0 = wb + lane, i1 = wb + 64 + lane;
+                if (i0 < n4) d[i0] = pack4(__builtin_nontemporal_load(s + i0));
+                if (i1 < n4) d[i1] = pack4(__builtin_nontemporal_load(s + i1));
+            }
         }
         return;
     }
+    const uint64_t stride = (uint64_t)p.grid_blocks * 256;
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < p.n; i += stride)
         reinterpret_cast<__attribute__((address_space(1))) uint16_t*>((uintptr_t)p.dst)[i] =
             (uint16_t)t0g::bf16_bits_ref(reinterpret_cast<const __attribute__((address_space(1))) float*>((uintptr_t)p.src)[i]);

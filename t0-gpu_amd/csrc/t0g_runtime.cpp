@@ -1691,10 +1691,13 @@ static int convert_locked(t0g_device *dev, uint64_t src, uint64_t dst, uint64_t 
     a.src = src;
     a.dst = dst;
     a.n = n;
-    const bool vec = (src & 31) == 0 && (dst & 15) == 0 && (n & 7) == 0;
+    const bool vec = (src & 15) == 0 && (dst & 7) == 0 && (n & 3) == 0;
     if (vec) a.flags |= T0G_CONVERT_VEC;
-    uint64_t blocks = ((vec ? n / 8 : n) + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
+    // vector form: 512 items of 4 elements per workgroup and grid step, one step
+    // per wave up to 2^20 workgroups; element form: 256 elements, 8192 workgroups
+    uint64_t blocks = vec ? (n / 4 + 511) / 512 : (n + 255) / 256;
+    const uint64_t cap = vec ? (1u << 20) : 8192;
+    if (blocks > cap) blocks = cap;
     a.grid_blocks = (uint32_t)blocks;
     return launch(dev, f, (uint32_t)blocks, 1, 1, 256, &a, sizeof a);
 }

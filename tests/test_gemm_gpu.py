@@ -809,17 +809,22 @@ def test_f32_to_bf16_is_the_reference_rounding(rt, bufs):
     special = np.array([0x3F808000, 0x3F818000, 0x3F80FFFF, 0x7F7FFFFF, 0x7F800000, 0xFF800000,
                         0x00000001, 0x807FFFFF, 0x7FC00000, 0x7FFFFFFF, 0x00000000, 0x80000000],
                        dtype=np.uint32)
-    for n in (1 << 20, 1000003):
+    # vector path: 16-byte aligned source, 8-byte aligned destination, n % 4 == 0;
+    # the rest element-wise.  n = 1000004 and 2044 end in a partly filled wave.
+    # (n, source offset in f32, destination offset in bf16)
+    cases = [(1 << 20, 0, 0), (1 << 20, 1, 0), (1000003, 0, 0), (1000003, 1, 0), (1000004, 0, 0),
+             (1000004, 4, 4), (1000004, 0, 1), (2044, 0, 0), (4, 0, 0), (12, 4, 0)]
+    for n, soff, doff in cases:
         bits = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
-        bits[:special.size] = special
+        bits[:min(n, special.size)] = special[:n]
         x = bits.view(np.float32)
-        for off in (0, 1):                            # off = 1: unaligned source, scalar path
-            src = bufs.up(np.concatenate([np.zeros(off, np.float32), x]))
-            dst = bufs.alloc(2 * n + 64, fill=0)
-            rt.f32_to_bf16(src + 4 * off, dst, n)
-            rt.wait_idle()
-            got = rt.read(dst, (n,), np.uint16)
-            assert np.array_equal(got, o.f32_to_bf16_rne(x)), f"n={n} off={off}"
+        src = bufs.up(np.concatenate([np.zeros(soff, np.float32), x]))
+        dst = bufs.alloc(2 * (n + doff) + 64, fill=0)
+        rt.f32_to_bf16(src + 4 * soff, dst + 2 * doff, n)
+        rt.wait_idle()
+        got = rt.read(dst, (n + doff + 32,), np.uint16)
+        assert np.array_equal(got[doff:doff + n], o.f32_to_bf16_rne(x)), f"n={n} soff={soff} doff={doff}"
+        assert not got[:doff].any() and not got[doff + n:].any(), f"n={n}: write outside [dst, dst + 2n)"
     assert o.f32_to_bf16_rne(np.array([0x7FFFFFFF], np.uint32).view(np.float32))[0] == 0x8000
 
 
