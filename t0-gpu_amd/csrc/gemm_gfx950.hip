@@ -1353,52 +1353,58 @@ __device__ __forceinline__ void splitk_reduce(const T0gReduceArgs& p) {
     const __attribute__((address_space(1))) float* ws = reinterpret_cast<const __attribute__((address_space(1))) float*>(p.ws);
     const __attribute__((address_space(1))) float* bias =
         reinterpret_cast<const __attribute__((address_space(1))) float*>(p.bias);
-    if (p.flags & T0G_REDUCE_VEC8) {
-        // 8 columns per thread: two 16-byte non-temporal loads per plane, four
-        // planes in flight, one 16-byte (bf16) or two (f32) stores
-        const uint32_t no = p.n >> 3;
-        const uint64_t total = (uint64_t)p.m * no;
-        for (uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += (uint64_t)p.grid_blocks * 256) {
-            const uint32_t row = (uint32_t)(q / no), col = (uint32_t)(q - (uint64_t)row * no) * 8;
-            const uint64_t w = (uint64_t)row * p.ldw + col;
-            f32x4_t a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+    if (p.flags & T0G_REDUCE_WAVE) {
+        // Large outputs: each wave sums 128 items of 4 consecutive elements (of the
+        // row-major M x N output) per grid step.  Per plane a lane makes two 16-byte
+        // non-temporal loads, and each load instruction covers 1 KB of consecutive
+        // plane; four planes are in flight.  Two 4-element stores follow.  The
+        // workgroups cover the output in one step up to the grid cap.
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        typedef const __attribute__((address_space(1))) f32x4_t gf32x4_t;
+        const uint64_t nq = p.n >> 2, total = (uint64_t)p.m * nq;
+        const uint32_t lane = threadIdx.x & 63u;
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const uint64_t step = (uint64_t)p.grid_blocks * 4 * 128;
+        for (uint64_t wb = ((uint64_t)blockIdx.x * 4 + wave) * 128; wb < total; wb += step) {
+            uint64_t item[2] = {wb + lane, wb + 64 + lane};
+            bool live[2] = {item[0] < total, item[1] < total};
+            f32x4_t acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
             for (uint32_t s0 = 0; s0 < p.splits; s0 += 4) {
                 f32x4_t v[4][2];
 #pragma unroll
                 for (uint32_t u = 0; u < 4; ++u)
-                    if (s0 + u < p.splits) {
-                        const __attribute__((address_space(1))) f32x4_t* src =
-                            reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>(
-                                ws + (s0 + u) * p.plane_elems + w);
-                        v[u][0] = __builtin_nontemporal_load(src);
-                        v[u][1] = __builtin_nontemporal_load(src + 1);
-                    }
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        if (s0 + u < p.splits && live[h])
+                            v[u][h] = __builtin_nontemporal_load(
+                                reinterpret_cast<gf32x4_t*>(ws + (s0 + u) * p.plane_elems) + item[h]);
 #pragma unroll
                 for (uint32_t u = 0; u < 4; ++u)
-                    if (s0 + u < p.splits) {
-                        a0 = a0 + v[u][0];
-                        a1 = a1 + v[u][1];
-                    }
+                    if (s0 + u < p.splits)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) acc[h] = acc[h] + v[u][h];
             }
-            float x[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-            float bv[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) bv[c] = (p.flags & T0G_REDUCE_BIAS) ? bias[col + c] : 0.0f;
-            apply_epilogue_n<8>(x, bv, epi_of(p));
-            const uint64_t o = (uint64_t)row * p.ldc + col;
-            if constexpr (OUT_BF16) {
-                u32x4_t w4;
+            for (int h = 0; h < 2; ++h) {
+                if (!live[h]) continue;
+                const uint64_t row = item[h] / nq;
+                const uint32_t col = (uint32_t)(item[h] - row * nq) * 4;
+                float x[4] = {acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                float bv[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    w4[c] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2 * c]) |
-                            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2 * c + 1]) << 16);
-                *reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>((uintptr_t)(p.c + o * 2)) = w4;
-            } else {
-                const f32x4_t y0 = {x[0], x[1], x[2], x[3]}, y1 = {x[4], x[5], x[6], x[7]};
-                __attribute__((address_space(1))) f32x4_t* dst =
-                    reinterpret_cast<__attribute__((address_space(1))) f32x4_t*>((uintptr_t)(p.c + o * 4));
-                dst[0] = y0;
-                dst[1] = y1;
+                for (int c = 0; c < 4; ++c) bv[c] = (p.flags & T0G_REDUCE_BIAS) ? bias[col + c] : 0.0f;
+                apply_epilogue_n<4>(x, bv, epi_of(p));
+                const uint64_t o = row * p.ldc + col;
+                if constexpr (OUT_BF16) {
+                    const u32x2_t w2 = {(uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[0]) |
+                                            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[1]) << 16),
+                                        (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[2]) |
+                                            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x[3]) << 16)};
+                    *reinterpret_cast<__attribute__((address_space(1))) u32x2_t*>((uintptr_t)(p.c + o * 2)) = w2;
+                } else {
+                    *reinterpret_cast<__attribute__((address_space(1))) f32x4_t*>((uintptr_t)(p.c + o * 4)) =
+                        f32x4_t{x[0], x[1], x[2], x[3]};
+                }
             }
         }
         return;

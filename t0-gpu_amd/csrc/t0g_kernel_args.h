@@ -137,7 +137,7 @@ typedef struct T0gConvertArgs {
 #define T0G_TIMELINE_SLOTS 8192u
 #define T0G_REDUCE_VEC 1u       /* planes 16-byte aligned, N % 4 == 0, C rows aligned for 4 elements */
 #define T0G_REDUCE_BIAS 2u      /* the chain reads bias[col]                                     */
-#define T0G_REDUCE_VEC8 4u      /* planes 32-byte aligned, N % 8 == 0, C rows aligned for 8 elements */
+#define T0G_REDUCE_WAVE 4u      /* as VEC; each wave takes 512 consecutive elements per step     */
 #define T0G_CONVERT_VEC 1u      /* src 16-byte and dst 8-byte aligned, n % 4 == 0: 16-byte loads */
 
 /* Epilogue chain operations: tile_ir's EpilogueOp (src/t0/tile_ir.rs:41-62),
