@@ -729,15 +729,19 @@ def test_epilogue_chains(rt, bufs, chain, preset, layout, m, n, k):
     assert np.array_equal(c16, o.f32_to_bf16_rne(c32)), "bf16 output is not RNE of the f32 output"
 
 
-@pytest.mark.parametrize("split_k,m,n", [(4, 256, 320), (16, 256, 320), (4, 512, 4096)])
-def test_epilogue_chain_after_split_k_reduce(rt, bufs, split_k, m, n):
-    """With split-K the chain runs once, in the plane-ordered reduce (4-wide, and
-    8-wide for the 512 x 4096 output)."""
-    k = 4096
+@pytest.mark.parametrize("split_k,m,n,ldc", [(4, 256, 320, 0), (16, 256, 320, 0), (4, 512, 4096, 0),
+                                               (4, 1000, 2100, 2108)])
+def test_epilogue_chain_after_split_k_reduce(rt, bufs, split_k, m, n, ldc):
+    """With split-K the chain runs once, in the plane-ordered reduce: the 4-wide form,
+    and for outputs of 2^21 elements or more the wave-contiguous one (512 x 4096:
+    whole rows per wave; 1000 x 2100 with a padded C: 525 items of 4 per row, so waves
+    cross rows and the last one is partly filled)."""
+    k = 4096 if m * n < (1 << 21) or m == 512 else 1024
     chain = ("bias", "gelu", "scale", "clamp")
     a, b, a_st, b_st, bias = _chain_case(m, n, k, "NT", 21)
     ref = o.epilogue_chain(o.gemm("NT", a, b, m, n, k), chain, bias=bias, scale=2.0, clamp=(-1.0, 3.0))
-    kw = dict(epilogue_ops=list(chain), epi_scale=2.0, clamp=(-1.0, 3.0), bias=bufs.up(bias), split_k=split_k)
+    kw = dict(epilogue_ops=list(chain), epi_scale=2.0, clamp=(-1.0, 3.0), bias=bufs.up(bias), split_k=split_k,
+              ldc=ldc)
     c32 = run_gemm(rt, bufs, "NT", a_st, b_st, m, n, k, **kw)
     check_parity(c32, ref, k, f"chain after split {split_k}")
     c16 = run_gemm(rt, bufs, "NT", a_st, b_st, m, n, k, out=t0g.BF16, **kw)
