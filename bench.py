@@ -117,12 +117,13 @@ MLP_SHAPES = [("NN", 1024, 11008, 4096), ("NN", 1024, 4096, 11008), ("NT", 1024,
               ("NT", 1024, 4096, 11008), ("TN", 11008, 4096, 1024), ("TN", 4096, 11008, 1024)]
 
 
-def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False):
+def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False, clock=False):
     """Benchmark config 5: forward H = X W1, Y = H W2 (NN) and backward dH = dY W2^T,
     dX = dH W1^T (NT), dW2 = H^T dY, dW1 = X^T dH (TN); bf16 in/out.  configs: one
     GemmConfig per GEMM (in MLP_SHAPES order) instead of auto_select's.  grouped: the
     GEMMs that do not depend on each other go through t0g_gemm_group: H, then
-    {Y, dH, dW2}, then {dX, dW1}."""
+    {Y, dH, dW2}, then {dX, dW1}.  clock: also sample the shader clock while steps
+    run back to back."""
     bsz, d_in, d_hid = 1024, 4096, 11008
     g = torch.Generator(device="cuda").manual_seed(7)
     x = torch.randn((bsz, d_in), generator=g, device="cuda").to(torch.bfloat16)
@@ -164,9 +165,14 @@ def mlp_step(t0g, torch, rt, stream, steps, warmup, configs=None, grouped=False)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     flop = 6 * 2.0 * bsz * d_in * d_hid
-    return {"ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12,
-            "frac_of_peak": flop / (ms * 1e-3) / 1e12 / PEAK_TFLOPS,
-            "kernels": [t0g.gemm_kernel_name(d) for d in descs]}
+    out = {"ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+           "frac_of_peak": flop / (ms * 1e-3) / 1e12 / PEAK_TFLOPS,
+           "kernels": [t0g.gemm_kernel_name(d) for d in descs]}
+    if clock:
+        clk = sustained_clock(torch, step, 3.0)
+        out["clock"] = clk if clk is not None else {"sclk_mhz_median": None}
+        out["clock"].update(_mfma_util(out["tflops"], out["clock"].get("sclk_mhz_median")))
+    return out
 
 
 def _event_ms(torch, stream, fn, steps, warmup):
@@ -503,8 +509,8 @@ def main():
     ap.add_argument("--no-clock", action="store_true", help="skip the shader-clock sampling (amd-smi) lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--clock", action="store_true",
-                    help="with --only LAYOUT:M:N:K: also sample the shader clock and socket power (amd-smi) "
-                         "while that GEMM runs back to back, and the MFMA utilisation they imply")
+                    help="with --only LAYOUT:M:N:K or MLP: also sample the shader clock and socket power (amd-smi) "
+                         "while that GEMM (or step) runs back to back, and the MFMA utilisation they imply")
     ap.add_argument("--timeline", action="store_true",
                     help="with --only LAYOUT:M:N:K: also record one launch's per-workgroup timeline (entry, end "
                          "of the K loop, stores done; t0g_set_timeline) and print its per-XCD summary")
@@ -582,9 +588,13 @@ def main():
         return
 
     if args.only and args.only.upper() in ("MLP", "MLP_GROUPED"):
-        r = mlp_step(t0g, torch, rt, stream, args.steps, args.warmup, grouped=args.only.upper() == "MLP_GROUPED")
-        print(json.dumps({"only": args.only, "ms_per_step": round(r["ms_per_step"], 5), "tflops": round(r["tflops"], 2),
-                          "frac_of_peak": round(r["frac_of_peak"], 4), "kernels": r["kernels"]}), flush=True)
+        r = mlp_step(t0g, torch, rt, stream, args.steps, args.warmup, grouped=args.only.upper() == "MLP_GROUPED",
+                     clock=args.clock)
+        line = {"only": args.only, "ms_per_step": round(r["ms_per_step"], 5), "tflops": round(r["tflops"], 2),
+                "frac_of_peak": round(r["frac_of_peak"], 4), "kernels": r["kernels"]}
+        if "clock" in r:
+            line["clock"] = r["clock"]
+        print(json.dumps(line), flush=True)
         rt.set_stream(None)
         rt.close()
         return
