@@ -131,6 +131,7 @@ typedef struct T0gConvertArgs {
 #define T0G_FLAG_C_VEC 2u       /* C base, row pitch and split-plane stride are 16-byte aligned */
 #define T0G_FLAG_BIAS 4u        /* the chain reads bias[col]                                     */
 #define T0G_FLAG_TIMELINE 8u    /* record the workgroup's timeline in t0g_timeline (diagnostics)   */
+#define T0G_FLAG_C_CACHED 16u   /* 64x64 / 128x128 kernels: ordinary (not non-temporal) stores of C */
 /* t0g_timeline: T0G_TIMELINE_SLOTS entries of 4 u64 per linear workgroup id: clock at entry, at
  * the end of the K loop and after the epilogue's stores completed (s_memrealtime, 100 MHz),
  * then XCC_ID << 32 | HW_ID of the wave that wrote it. */
