@@ -883,6 +883,16 @@ struct DmaOperand<true, ROWS, NT, SUBS, BK> {
     __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
         return lds_load_b128(stage + frag[KK] + sub * 32 * kKRow);
     }
+    // The same for a K step known at run time (uniform): kstep_off(kk) once,
+    // then read_at per stage.  2*kk + g == 2*kk ^ g and the row offset has
+    // zero chunk bits, so frag[kk] == frag[0] ^ (kk << 5).  Computed, not
+    // selected from frag[]: a run-time index into the array makes the
+    // compiler place it in LDS (18 KB more LDS, a store and reload in the
+    // prologue, which cost the thin shapes 7 us per call).
+    __device__ __forceinline__ uint32_t kstep_off(uint32_t kk) const { return frag[0] ^ (kk << 5); }
+    __device__ __forceinline__ bf16x8_t read_at(uint32_t stage, int sub, uint32_t koff) const {
+        return lds_load_b128(stage + koff + sub * 32 * kKRow);
+    }
     template <int KK>
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
 #pragma unroll
@@ -950,6 +960,17 @@ struct DmaOperand<false, ROWS, NT, SUBS, BK> {
     __device__ __forceinline__ void read(uint32_t stage, bf16x8_t (&f)[SUBS]) const {
 #pragma unroll
         for (int sub = 0; sub < SUBS; ++sub) f[sub] = read_one<KK>(stage, sub);
+    }
+    __device__ __forceinline__ uint32_t kstep_off(uint32_t kk) const { return kk * 16 * kRowB; }
+    __device__ __forceinline__ bf16x8_t read_at(uint32_t stage, int sub, uint32_t koff) const {
+        short v[8];
+        short(&lo)[4] = *reinterpret_cast<short(*)[4]>(&v[0]);
+        short(&hi)[4] = *reinterpret_cast<short(*)[4]>(&v[4]);
+        lds_load_tr16(stage + frag[sub] + koff, lo);
+        lds_load_tr16(stage + frag[sub] + koff + 4 * kRowB, hi);
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8s w = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+        return __builtin_bit_cast(bf16x8_t, w);
     }
     template <int KK>
     __device__ __forceinline__ bf16x8_t read_one(uint32_t stage, int sub) const {
@@ -1239,6 +1260,116 @@ __device__ __forceinline__ void k_pipeline_deep(f32x16_t (&acc)[SM][SN], const O
     }
 }
 
+// K split across the waves (64x64 deep kernels): wave w multiplies the whole
+// 64x64 tile (2 x 2 blocks of 32x32) for K step w of every 64-K stage, so each
+// A and B row is read from LDS once per stage (4 fragment reads per wave
+// instead of the 8 of the 2 x 2 wave grid, where every row was read by two
+// waves).  The LDS DMA of a stage and the fragment reads of the next share the
+// CU's LDS; halving the reads took the C4a loop from 10.0 to 8.4 us in a
+// standalone model of this kernel, and a C4a call (128 x 4096 x 4096 NT,
+// split 2, plus the reduce) from 14.2 to 13.75 us.  Fragments of the next stage are read one
+// stage ahead, as in k_pipeline_deep; the four DMA instructions of the stage
+// being filled go one behind each MFMA.  ksplit_sum() then adds the four
+// partial tiles in wave order.
+template <bool CHECK, int NS, uint32_t A_BYTES, uint32_t STAGE, int kVmemPerStage, class OpA, class OpB>
+__device__ __forceinline__ void k_pipeline_ksplit(f32x16_t (&acc)[2][2], const OpA& la, const OpB& lb,
+                                                  const T0gGemmArgs& p, uint32_t a_bytes, uint32_t b_bytes,
+                                                  uint32_t kbeg, uint32_t kend, int nst, uint32_t lds0) {
+    static_assert(NS >= 4, "ring of at least 4 stages");
+    static_assert(kVmemPerStage == 4, "one DMA instruction behind each of the four MFMAs");
+    constexpr uint32_t BK = 64;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ka = la.kstep_off(w), kb = lb.kstep_off(w);
+    auto read4 = [&](uint32_t stage, bf16x8_t (&fa)[2], bf16x8_t (&fb)[2]) {
+        fa[0] = la.read_at(stage, 0, ka);
+        fa[1] = la.read_at(stage, 1, ka);
+        fb[0] = lb.read_at(stage + A_BYTES, 0, kb);
+        fb[1] = lb.read_at(stage + A_BYTES, 1, kb);
+    };
+    auto issue_q = [&](int q, u32x4_t ra, u32x4_t rb, uint32_t fill, uint32_t kf) {
+        if (q < OpA::kInstr)
+            la.template issue_one<CHECK>(q, ra, fill, kf, kend);
+        else
+            lb.template issue_one<CHECK>(q - OpA::kInstr, rb, fill + A_BYTES, kf, kend);
+    };
+    // one stage: read stage `nxt` into (na, nb), multiply (fa, fb) with the
+    // DMA of stage kf into `fill` behind the MFMAs, wait for the stage two
+    // ahead and meet at the barrier
+    auto stage_step = [&](const bf16x8_t (&fa)[2], const bf16x8_t (&fb)[2], bf16x8_t (&na)[2], bf16x8_t (&nb)[2],
+                          uint32_t nxt, uint32_t fill, uint32_t kf) {
+        read4(nxt, na, nb);
+        const u32x4_t ra = la.rsrc(p.a, a_bytes, p.lda, kf);
+        const u32x4_t rb = lb.rsrc(p.b, b_bytes, p.ldb, kf);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                issue_q(i * 2 + j, ra, rb, fill, kf);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));   // the stage two ahead has landed
+        barrier_no_fence();
+    };
+    bf16x8_t fa0[2], fb0[2], fa1[2], fb1[2];
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        la.template issue<CHECK>(lds0 + s * STAGE, p.a, a_bytes, p.lda, kbeg + s * BK, kend);
+        lb.template issue<CHECK>(lds0 + s * STAGE + A_BYTES, p.b, b_bytes, p.ldb, kbeg + s * BK, kend);
+    }
+    T0G_WAIT_VMCNT(kVmemPerStage * (NS - 3));
+    barrier_no_fence();
+    read4(lds0, fa0, fb0);
+
+    uint32_t cur = 0;
+    uint32_t fill = (NS - 1) * STAGE;
+    for (int s = 0; s < nst; s += 2) {
+        {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            stage_step(fa0, fb0, fa1, fb1, lds0 + nxt, lds0 + fill, kbeg + (uint32_t)(s + NS - 1) * BK);
+            fill = cur;
+            cur = nxt;
+        }
+        if (s + 1 < nst) {
+            const uint32_t nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
+            stage_step(fa1, fb1, fa0, fb0, lds0 + nxt, lds0 + fill, kbeg + (uint32_t)(s + NS) * BK);
+            fill = cur;
+            cur = nxt;
+        }
+    }
+}
+
+// Sum the four waves' partial 64x64 tiles (each 2 x 2 blocks of 32x32 in the
+// MFMA result layout) through LDS, in wave order ((w0 + w1) + w2) + w3, and
+// return wave w's own 32x32 block (block w = the quadrant (w / 2, w % 2) the
+// 2 x 2 wave grid's epilogue stores).  Needs 64 KB of LDS at `lds`; callers
+// have finished with the ring (vmcnt(0) and a barrier).  Every wave writes all
+// four blocks and reads four: a form that writes and reads only the three
+// foreign blocks, with no barrier after the reads, ran 0.5-0.9 us slower per
+// call on the thin shapes.  It ends with a barrier, before the epilogue reuses
+// the LDS.
+__device__ __forceinline__ f32x16_t ksplit_sum(const f32x16_t (&acc)[2][2], uint32_t lds) {
+    typedef __attribute__((address_space(3))) float lds_f32;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            *reinterpret_cast<lds_f32*>((uintptr_t)(lds + ((w * 4 + b) * 1024 + e * 64 + lane) * 4)) = acc[b >> 1][b & 1][e];
+    __syncthreads();
+    f32x16_t r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        float v = 0.0f;
+#pragma unroll
+        for (int src = 0; src < 4; ++src)
+            v = v + *reinterpret_cast<const lds_f32*>((uintptr_t)(lds + ((src * 4 + w) * 1024 + e * 64 + lane) * 4));
+        r[e] = v;
+    }
+    __syncthreads();
+    return r;
+}
+
 }  // namespace t0g
 
 #include "gemm_red.h"
@@ -1250,7 +1381,7 @@ namespace t0g {
 // LDS by DMA (k_pipeline), epilogue staged through LDS.  RED: split-K reduced
 // inside the kernel (ra: the launch's T0gGemmRedArgs, p = ra->g).
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool A_K, bool B_K, bool OUT_BF16, uint32_t BK, int NS,
-          bool RED = false>
+          bool RED = false, bool KS = false>
 __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGemmRedArgs* ra = nullptr) {
     constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -1296,12 +1427,35 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
     for (int i = 0; i < SM; ++i)
 #pragma unroll
         for (int j = 0; j < SN; ++j) acc[i][j] = f32x16_t{};
+    // KS (64x64 deep ring only): K split across the waves (k_pipeline_ksplit),
+    // whole-tile partials summed by ksplit_sum() after the loop.  The host
+    // takes these kernels (suffix _ds, _dsr) for K ranges of 24 stages or more.
+    constexpr bool KSPLIT = KS;
+    static_assert(!KS || (BK == 64 && SM * SN == 1), "K split across the waves: 64x64 deep ring only");
+    f32x16_t acc4[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc4[i][j] = f32x16_t{};
 
     if (nst > 0) {
         const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
         // Stages past a K tail need masked DMA; whole stages (the usual case)
         // skip the per-lane bound test.
-        if constexpr (BK == 64 && SM * SN == 1) {
+        if constexpr (KSPLIT) {
+            static_assert(WAVES_M == 2 && WAVES_N == 2, "four waves, one K step each");
+            // operands with both 32-row sub-tiles of the tile, from row 0
+            DmaOperand<A_K, BM, NT, 2, BK> ka;
+            DmaOperand<B_K, BN, NT, 2, BK> kb;
+            ka.init(tid, m0, p.lda, 0, l32, g);
+            kb.init(tid, n0, p.ldb, 0, l32, g);
+            if ((kend - kbeg) % BK == 0)
+                k_pipeline_ksplit<false, NS, A_BYTES, STAGE, kVmemPerStage>(acc4, ka, kb, p, a_bytes, b_bytes, kbeg,
+                                                                            kend, nst, lds0);
+            else
+                k_pipeline_ksplit<true, NS, A_BYTES, STAGE, kVmemPerStage>(acc4, ka, kb, p, a_bytes, b_bytes, kbeg,
+                                                                           kend, nst, lds0);
+        } else if constexpr (BK == 64 && SM * SN == 1) {
             if ((kend - kbeg) % BK == 0)
                 k_pipeline_deep<false, NS, A_BYTES, STAGE, kVmemPerStage>(acc, la, lb, p, a_bytes, b_bytes, kbeg,
                                                                           kend, nst, lds0);
@@ -1323,6 +1477,10 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
     static_assert((NT / 64) * VecEpilogue<SN>::kWaveBytes <= NS * STAGE, "epilogue staging must fit the LDS ring");
     T0G_WAIT_VMCNT(0);    // LDS DMA still in flight (stages past K) has landed
     barrier_no_fence();   // and every wave is done with the ring
+    if constexpr (KSPLIT) {
+        static_assert(4 * 4 * 16 * 64 * 4 <= NS * STAGE, "the partial tiles must fit the LDS ring");
+        acc[0][0] = ksplit_sum(acc4, lds_addr(smem));
+    }
     tl_mark(p, 1);
     if constexpr (RED) {
         // the partial tile, raw fp32, row-major into this workgroup's slot
@@ -1665,6 +1823,23 @@ T0G_GEMM_TILE_U(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_D(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_D(t0g_gemm_128x128_k64, 128, 128, 2, 2)
 
+// The 64x64 deep ring with K split across the four waves (suffix _ds): each
+// wave multiplies the whole tile for one 16-wide K step of every stage, and the
+// four partial tiles are summed through LDS after the loop.  For K ranges of
+// 24 stages or more (the host's choice; the sum does not pay for shorter ones).
+#define T0G_GEMM_DS(NAME, AK, BKM, OBF)                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))             \
+        NAME(T0gGemmArgs p) {                                                                                 \
+        t0g::gemm_tile_fast<64, 64, 2, 2, AK, BKM, OBF, T0G_PIPE_D_64x64, false, true>(p);                    \
+    }
+#define T0G_GEMM_LAYOUTS_DS(OUTN, OBF)                                       \
+    T0G_GEMM_DS(t0g_gemm_64x64_k64_nt_##OUTN##_ds, true, true, OBF)          \
+    T0G_GEMM_DS(t0g_gemm_64x64_k64_nn_##OUTN##_ds, true, false, OBF)         \
+    T0G_GEMM_DS(t0g_gemm_64x64_k64_tn_##OUTN##_ds, false, false, OBF)        \
+    T0G_GEMM_DS(t0g_gemm_64x64_k64_tt_##OUTN##_ds, false, true, OBF)
+T0G_GEMM_LAYOUTS_DS(f32, false)
+T0G_GEMM_LAYOUTS_DS(bf16, true)
+
 // Deep-ring kernels with the split-K reduced inside the kernel (suffix _dr).
 #define T0G_GEMM_DR(NAME, BM, BN, WM, WN, AK, BKM, OBF)                                                          \
     extern "C" __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))       \
@@ -1681,6 +1856,20 @@ T0G_GEMM_TILE_D(t0g_gemm_128x128_k64, 128, 128, 2, 2)
     T0G_GEMM_LAYOUTS_DR(PFX, BM, BN, WM, WN, bf16, true)
 T0G_GEMM_TILE_DR(t0g_gemm_64x64_k64, 64, 64, 2, 2)
 T0G_GEMM_TILE_DR(t0g_gemm_128x128_k64, 128, 128, 2, 2)
+
+// _ds with the split-K reduced inside the kernel (suffix _dsr).
+#define T0G_GEMM_DSR(NAME, AK, BKM, OBF)                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))             \
+        NAME(T0gGemmRedArgs ra) {                                                                             \
+        t0g::gemm_tile_fast<64, 64, 2, 2, AK, BKM, OBF, T0G_PIPE_D_64x64, true, true>(ra.g, &ra);             \
+    }
+#define T0G_GEMM_LAYOUTS_DSR(OUTN, OBF)                                      \
+    T0G_GEMM_DSR(t0g_gemm_64x64_k64_nt_##OUTN##_dsr, true, true, OBF)        \
+    T0G_GEMM_DSR(t0g_gemm_64x64_k64_nn_##OUTN##_dsr, true, false, OBF)       \
+    T0G_GEMM_DSR(t0g_gemm_64x64_k64_tn_##OUTN##_dsr, false, false, OBF)      \
+    T0G_GEMM_DSR(t0g_gemm_64x64_k64_tt_##OUTN##_dsr, false, true, OBF)
+T0G_GEMM_LAYOUTS_DSR(f32, false)
+T0G_GEMM_LAYOUTS_DSR(bf16, true)
 
 extern "C" __global__ void __launch_bounds__(256) t0g_splitk_reduce_f32(T0gReduceArgs p) {
     t0g::splitk_reduce<false>(p);

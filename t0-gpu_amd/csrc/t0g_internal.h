@@ -18,6 +18,8 @@ constexpr uint32_t kTileK = 64;
 constexpr uint32_t kWaveSize = 64;
 constexpr uint32_t kNumCUs = 256;
 constexpr uint32_t kMaxSplitK = 64;
+// 64-K stages per split from which the 64x64 deep ring splits K across its waves
+constexpr uint32_t kKsplitMinStages = 24;
 constexpr double kPeakFlops = 2.5e15;   // dense bf16 MFMA, MI355X
 constexpr double kPeakBytes = 8.0e12;   // HBM3E, MI355X
 

@@ -404,9 +404,18 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     // the stream-K ones with a K-contiguous A (NN, NT), which keep the 8-wave
     // ping-pong schedule.
     p->wg = (tile->bm == 256 && !(stream_k && a_k_major(transpose))) ? 256u : tile->wg;
+    // The 64x64 deep ring splits K across its four waves (_ds, _dsr) for K
+    // ranges of kKsplitMinStages 64-K stages or more: the loop then reads each
+    // fragment once per stage instead of twice, and the closing sum of the four
+    // partial tiles (about 0.5 us) is paid back.  Per call, split against
+    // unsplit: 32 stages (128x4096x4096 NT, split 2) 13.8 against 14.2 us;
+    // 16 stages (256x256x1024 NT) 6.76 against 6.64 us; 4 stages (256^3)
+    // 4.91 against 4.30 us.
+    const bool ksplit = deep && tile->bm == 64 && (kps + 63) / 64 >= kKsplitMinStages;
+    const char *deep_sfx = ksplit ? (p->fused ? "_dsr" : "_ds") : (p->fused ? "_dr" : "_d");
     p->symbol = std::string(tile->symbol_prefix) + "_" + layout_tag(transpose) + "_" +
                 ((out_bf16 && (!partial || p->fused)) ? "bf16" : "f32") +
-                (aligned ? (wide ? "_x" : deep ? (p->fused ? "_dr" : "_d") : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");
+                (aligned ? (wide ? "_x" : deep ? deep_sfx : p->fused ? "_r" : "") : "_u") + (stream_k ? "_sk" : "");
     if ((uint64_t)p->tiles_m * p->tiles_n > 0x7FFFFFFFull)
         return fail(T0G_ERR_INVALID_ARG, "too many output tiles (%u x %u)", p->tiles_m, p->tiles_n);
     if (stream_k && (uint64_t)p->tiles_m * p->tiles_n * p->sk_ipt > 0x7FFFFFFFull)

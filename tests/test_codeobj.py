@@ -48,7 +48,9 @@ def _gfx950_elf(blob):
     ("t0g_gemm_256x256_k64_nt_f32", 104, 131072, 256),
     ("t0g_gemm_256x256_k64_tn_bf16", 104, 131072, 256),
     ("t0g_gemm_128x128_k64_nn_f32", 104, None, 256),
-    ("t0g_gemm_64x64_k64_nt_f32_d", 104, None, 256),
+    ("t0g_gemm_64x64_k64_nt_f32_d", 104, 131072, 256),
+    ("t0g_gemm_64x64_k64_nn_bf16_ds", 104, 131072, 256),
+    ("t0g_gemm_64x64_k64_tn_f32_dsr", 144, None, 256),
     ("t0g_gemm_256x256_k64_nn_bf16_sk", 144, None, 512),
     ("t0g_gemm_256x256_k64_tt_f32_sk", 144, None, 256),
     ("t0g_gemm_256x256_k64_nn_bf16_r", 144, None, 256),
@@ -80,7 +82,7 @@ def test_argument_block_sizes_match_the_header(blob):
                     names.add(part[:-3].decode())
     assert len(names) >= 60
     for s in sorted(names):
-        want = 144 if s.endswith(("_sk", "_r", "_dr")) else 104   # T0gGemmSkArgs / T0gGemmRedArgs
+        want = 144 if s.endswith(("_sk", "_r", "_dr", "_dsr")) else 104   # T0gGemmSkArgs / T0gGemmRedArgs
         assert t0g.code_object_kernel_meta(blob, s).kernarg_size == want, s
 
 

@@ -284,11 +284,16 @@ def test_split_k_mode_selects_the_reduction():
     c64 = t0g.GemmConfig.preset("gfx950_64x64_k64")
     # 32 tiles x 8 slices: one workgroup per CU, so the deep-ring kernel writes the planes
     assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
+    assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_f32_ds"     # 32 stages per split
+    assert name(m=64, n=512, config=c64, split_k=4) == "t0g_gemm_64x64_k64_nt_f32_d"   # 16
     t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
     try:
         assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_dr"
         assert name(m=256, config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_r"   # 512 workgroups
-        assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_bf16_dr"
+        # 2048 K per split (32 stages of 64): the deep ring with K split across its waves
+        assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_bf16_dsr"
+        assert name(m=64, n=512, config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_bf16_dsr"
+        assert name(m=64, n=512, config=c64, split_k=4) == "t0g_gemm_64x64_k64_nt_bf16_dr"   # 16 stages
         assert name(config=c64, split_k=16) == "t0g_gemm_64x64_k64_nt_f32"       # 2048 workgroups: no _r kernel
         assert name(m=64, n=512, config=c64, split_k=16) == "t0g_gemm_64x64_k64_nt_bf16_dr"
         assert name(m=64, n=512, config=c64, split_k=32) == "t0g_gemm_64x64_k64_nt_f32_d"   # 128-element chunks

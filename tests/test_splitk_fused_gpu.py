@@ -101,9 +101,15 @@ def test_fused_equals_reduce_kernel(rt, layout, m, n, k, cfg, sk, out):
     try:
         name_f, fused = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_IN_KERNEL)
         name_r, planes = _run(rt, da, db, m, n, k, layout, cfg, sk, out, t0g.SPLIT_K_REDUCE_KERNEL)
-        assert name_f.endswith(("_r", "_dr")) and not name_r.endswith(("_r", "_dr")), (name_f, name_r)
-        assert name_f.endswith("_dr") == (cfg.tile_m < 256 and (m + cfg.tile_m - 1) // cfg.tile_m *
-                                          ((n + cfg.tile_n - 1) // cfg.tile_n) * sk <= 256), name_f
+        fused_sfx = ("_r", "_dr", "_dsr")
+        assert name_f.endswith(fused_sfx) and not name_r.endswith(fused_sfx), (name_f, name_r)
+        deep = cfg.tile_m < 256 and (m + cfg.tile_m - 1) // cfg.tile_m * ((n + cfg.tile_n - 1) // cfg.tile_n) * sk <= 256
+        assert name_f.endswith(("_dr", "_dsr")) == deep, name_f
+        # the 64x64 deep ring splits K across its waves from 24 stages of 64 per slice,
+        # in both modes alike
+        stages = ((k + sk - 1) // sk + 63) // 64   # 64-K stages per slice (slices round up to whole stages)
+        ksplit = deep and cfg.tile_m == 64 and stages >= 24
+        assert name_f.endswith("_dsr") == ksplit and name_r.endswith("_ds") == ksplit, (name_f, name_r)
         assert np.array_equal(fused, planes), f"{name_f} differs from planes + reduce kernel"
         got = fused if out == t0g.F32 else o.bf16_to_f32(fused)
         ok, relf, maxabs, bound = o.parity(got, o.gemm("NT", a_mk, b_nk, m, n, k), k)
