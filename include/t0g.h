@@ -581,16 +581,20 @@ T0G_API int t0g_set_stream_k_spin_limit(uint32_t polls);
  * sums the whole tile (the result does not change). */
 T0G_API int t0g_debug_stream_k_stall(int on);
 /* How t0g_gemm runs split-K (no reference counterpart; the reference sums the
- * planes on the host): T0G_SPLIT_K_REDUCE_KERNEL (0, the default) = fp32 planes
+ * planes on the host): T0G_SPLIT_K_REDUCE_KERNEL (0) = fp32 planes
  * ([splits][M][N] in desc->workspace) plus the reduce kernel;
  * T0G_SPLIT_K_IN_KERNEL (1) = reduced inside the GEMM kernel wherever the plan
  * allows it (one launch; the K slices of a tile sum it in plane order), else as
- * 0.  Both give the same bits.  The in-kernel form moves every partial through
- * HBM twice while the tile's slices wait for each other; measured on MI355X it
- * is slower than the two launches on the thin shapes and level on the MLP's,
- * hence not the default.  Process-wide, for later calls. */
+ * 0; T0G_SPLIT_K_AUTO (2, the default) = in the kernel for two K slices on the
+ * 64x64 and 128x128 deep-ring kernels (the second slice to finish adds the
+ * first's partial, with no wait), else as 0.  All give the same bits.  With
+ * more slices the in-kernel form is slower than the two launches on MI355X
+ * (the slices wait for each other, and every partial crosses HBM twice); with
+ * two it is faster (128x4096x4096: 13.8 against 14.1 us).  Process-wide, for
+ * later calls. */
 #define T0G_SPLIT_K_REDUCE_KERNEL 0u
 #define T0G_SPLIT_K_IN_KERNEL 1u
+#define T0G_SPLIT_K_AUTO 2u
 T0G_API int t0g_set_split_k_mode(uint32_t mode);
 /* Workgroup timeline, a diagnostic with no reference counterpart (the
  * reference times whole dispatches on the host clock).  on != 0: later

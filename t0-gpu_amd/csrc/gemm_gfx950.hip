@@ -426,9 +426,16 @@ struct VecEpilogue {
 
 // WT: the 16-byte stores write through to memory (sc0 sc1) instead of going
 // non-temporal into this XCD's L2, for data that workgroups on other XCDs read.
-template <int SM, int SN, bool OUT_BF16, bool WT = false, bool CACHED = false>
+// PAIR: before the epilogue, add the tile's other K slice of a two-slice split:
+// `partner` addresses that slice's fp32 partial at this wave tile's first
+// element, row-major with `pld` floats per row, written through to memory by
+// another workgroup; it is read past the caches (volatile: sc0 sc1) and added
+// in plane order, (0 + p0) + p1, with own_first telling whether this
+// workgroup's own values are p0.
+template <int SM, int SN, bool OUT_BF16, bool WT = false, bool CACHED = false, bool PAIR = false>
 __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x16_t (&acc)[SM][SN], uint32_t row0,
-                                               uint32_t col0, uint32_t lane, uint32_t lds, bool vec, uint32_t split) {
+                                               uint32_t col0, uint32_t lane, uint32_t lds, bool vec, uint32_t split,
+                                               uint64_t partner = 0, uint32_t pld = 0, bool own_first = false) {
     typedef VecEpilogue<SN> E;
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) float lds_f32;
@@ -436,9 +443,23 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
     constexpr int kCols = OUT_BF16 ? 8 : 4;              // columns per lane and store
     constexpr int kLanesPerRow = E::kWTN / kCols;
     constexpr int kRowsPerPass = 64 / kLanesPerRow;
+    constexpr int kPasses = 32 / kRowsPerPass;
     static_assert(kLanesPerRow <= 64 && 64 % kLanesPerRow == 0, "row must map onto whole lanes");
     const uint32_t l32 = lane & 31u, g = lane >> 5;
     const uint32_t rl = lane / kLanesPerRow, cl = (lane % kLanesPerRow) * kCols;
+    // the partner's values for every (block, pass) this lane stores, all loads in flight at once
+    f32x4_t pv[PAIR ? SM : 1][PAIR ? kPasses : 1][PAIR ? kCols / 4 : 1];
+    if constexpr (PAIR) {
+        typedef volatile __attribute__((address_space(1))) f32x4_t gvf32x4_t;
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int pass = 0; pass < kPasses; ++pass)
+#pragma unroll
+                for (int c = 0; c < kCols; c += 4)
+                    pv[i][pass][c / 4] = *reinterpret_cast<gvf32x4_t*>(
+                        (uintptr_t)(partner + ((uint64_t)(i * 32 + pass * kRowsPerPass + rl) * pld + cl + c) * 4u));
+    }
     float bv[kCols];
 #pragma unroll
     for (int c = 0; c < kCols; ++c) bv[c] = 0.0f;
@@ -463,7 +484,7 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
             }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int pass = 0; pass < 32 / kRowsPerPass; ++pass) {
+        for (int pass = 0; pass < kPasses; ++pass) {
             const uint32_t rr = pass * kRowsPerPass + rl;
             float v[kCols];
 #pragma unroll
@@ -473,6 +494,13 @@ __device__ __forceinline__ void store_tile_vec(const T0gGemmArgs& p, const f32x1
                 v[c + 1] = q[1];
                 v[c + 2] = q[2];
                 v[c + 3] = q[3];
+            }
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int c = 0; c < kCols; ++c) {
+                    const float o = pv[i][pass][c / 4][c % 4];
+                    v[c] = own_first ? (0.0f + v[c]) + o : (0.0f + o) + v[c];
+                }
             }
             apply_epilogue_n<kCols>(v, bv, epi_of(p));
             const uint32_t grow = row0 + i * 32 + rr, gcol = col0 + cl;
@@ -1494,7 +1522,11 @@ __device__ __forceinline__ void gemm_tile_fast(const T0gGemmArgs& p, const T0gGe
                                             lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes, true, 0);
         T0G_WAIT_VMCNT(0);    // the partial's stores have reached memory
         barrier_no_fence();
-        red_finish<BM, BN, NT, OUT_BF16>(*ra, gp.tile, gp.split, m0, n0, lds_addr(smem), NS * STAGE);
+        if (ra->splits == 2u)
+            red_pair<BM, BN, SM, SN, OUT_BF16>(*ra, acc, gp.tile, gp.split, m0, n0, wm * WTM, wn * WTN, lane,
+                                               lds_addr(smem) + wave * VecEpilogue<SN>::kWaveBytes);
+        else
+            red_finish<BM, BN, NT, OUT_BF16>(*ra, gp.tile, gp.split, m0, n0, lds_addr(smem), NS * STAGE);
     } else {
         const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
         // the store form is chosen once per tile (a test of the flag next to each

@@ -206,6 +206,39 @@ __device__ __forceinline__ void red_finish(const T0gGemmRedArgs& ra, uint32_t ti
     }
 }
 
+// Two K slices: no wait at all.  Both workgroups of the tile have written
+// their partials through to memory (vmcnt(0), then a barrier) when thread 0
+// increments the tile's arrival counter.  The first to arrive leaves.  The
+// second finds the other slice's partial complete in memory, adds it to its
+// own values in plane order -- (0 + p0) + p1, the reduce kernel's order, so
+// the bits equal the two-kernel path's whichever slice arrives second -- and
+// stores the output through the epilogue; it also clears the counter for the
+// next launch (both workgroups are done with it).  This takes three memory
+// round trips after the K loop (partial, counter, the other partial), where
+// red_finish's arrival, wait, claim and done counter take six.
+template <int BM, int BN, int SM, int SN, bool OUT_BF16>
+__device__ __forceinline__ void red_pair(const T0gGemmRedArgs& ra, const f32x16_t (&acc)[SM][SN], uint32_t tile,
+                                         uint32_t split, uint32_t m0, uint32_t n0, uint32_t wrow, uint32_t wcol,
+                                         uint32_t lane, uint32_t lds_stage) {
+    __shared__ uint32_t s_pair;
+    const T0gGemmArgs& p = ra.g;
+    gred_u32_t* const ctl = reinterpret_cast<gred_u32_t*>((uintptr_t)ra.sync);
+    gred_u32_t* const arrival = ctl + T0G_RED_ARRIVAL + tile * T0G_RED_LINE_WORDS;
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(arrival, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev >= 2u) __hip_atomic_fetch_add(ctl + T0G_SK_TIMEOUTS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == 1u) __hip_atomic_store(arrival, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_pair = prev;
+    }
+    __syncthreads();
+    if (s_pair != 1u) return;
+    constexpr uint32_t kSlot = (uint32_t)BM * BN * 4u;
+    const uint64_t partner = ra.partials + (uint64_t)(tile * 2u + (split ^ 1u)) * kSlot + ((uint64_t)wrow * BN + wcol) * 4u;
+    const bool vec = (p.flags & T0G_FLAG_C_VEC) && m0 + BM <= p.m && n0 + BN <= p.n;
+    store_tile_vec<SM, SN, OUT_BF16, false, false, true>(p, acc, m0 + wrow, n0 + wcol, lane, lds_stage, vec, 0,
+                                                         partner, BN, split == 0u);
+}
+
 }  // namespace t0g
 
 #endif

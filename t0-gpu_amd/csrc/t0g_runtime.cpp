@@ -127,7 +127,7 @@ static std::atomic<uint32_t> g_sk_spin_limit{1u << 20};
 static std::atomic<uint32_t> g_sk_debug{0};
 // Split-K: 0 = reduce inside the GEMM kernel where the plan allows it (the _r
 // kernels), 1 = always partial planes plus the separate reduce kernel.
-static std::atomic<uint32_t> g_split_mode{T0G_SPLIT_K_REDUCE_KERNEL};
+static std::atomic<uint32_t> g_split_mode{T0G_SPLIT_K_AUTO};
 // Workgroup timeline recording (t0g_set_timeline): a diagnostic, off by default.
 static std::atomic<int> g_timeline{0};
 // Polls a workgroup of a fused split-K launch waits for its tile's other K
@@ -395,7 +395,11 @@ static int make_plan(const TileDef *tile, uint32_t transpose, bool out_bf16, Ope
     // (a slice waits only for slices running at the same time) and slots
     // addressable by a 32-bit buffer descriptor.  The 64x64 tile has it in its
     // deep-ring kernel only.
-    p->fused = partial && allow_fused && g_split_mode.load() == T0G_SPLIT_K_IN_KERNEL && aligned && !wide && !stream_k &&
+    // T0G_SPLIT_K_AUTO: in the kernel for two slices on the deep rings, whose
+    // red_pair finish has the second slice add the first's partial without a wait
+    const uint32_t mode = g_split_mode.load();
+    const bool want_fused = mode == T0G_SPLIT_K_IN_KERNEL || (mode == T0G_SPLIT_K_AUTO && sk == 2 && deep);
+    p->fused = partial && allow_fused && want_fused && aligned && !wide && !stream_k &&
                (tile->bm != 64 || deep) && (sk & (sk - 1)) == 0 && sk <= kMaxSplitK &&
                (uint64_t)sk * 256 <= (uint64_t)tile->bm * tile->bn &&
                red_grid <= (uint64_t)kNumCUs * tile->wg_per_cu && red_grid <= T0G_RED_MAX_GRID &&
@@ -722,7 +726,8 @@ int t0g_debug_stream_k_stall(int on) {
 }
 
 int t0g_set_split_k_mode(uint32_t mode) {
-    if (mode > 1) return fail(T0G_ERR_INVALID_ARG, "split-K mode %u (0: reduce kernel, 1: in-kernel reduce)", mode);
+    if (mode > 2)
+        return fail(T0G_ERR_INVALID_ARG, "split-K mode %u (0: reduce kernel, 1: in-kernel reduce, 2: auto)", mode);
     g_split_mode.store(mode);
     return ok();
 }

@@ -537,12 +537,13 @@ def debug_stream_k_stall(on):
     _check(_lib.t0g_debug_stream_k_stall(1 if on else 0))
 
 
-SPLIT_K_REDUCE_KERNEL, SPLIT_K_IN_KERNEL = 0, 1
+SPLIT_K_REDUCE_KERNEL, SPLIT_K_IN_KERNEL, SPLIT_K_AUTO = 0, 1, 2
 
 
 def set_split_k_mode(mode):
-    """SPLIT_K_REDUCE_KERNEL (default): planes + reduce kernel; SPLIT_K_IN_KERNEL: split-K
-    reduced inside the GEMM kernel where the plan allows it.  Same bits either way."""
+    """SPLIT_K_REDUCE_KERNEL: planes + reduce kernel; SPLIT_K_IN_KERNEL: split-K reduced
+    inside the GEMM kernel where the plan allows it; SPLIT_K_AUTO (default): in the kernel
+    for two K slices on the deep-ring tiles, else planes.  Same bits every way."""
     _check(_lib.t0g_set_split_k_mode(mode))
 
 

@@ -376,7 +376,7 @@ def test_splitk_reduce_is_the_host_plane_order(rt, bufs, m, n, k, sk, out):
         rt.gemm_desc(d)
         rt.wait_idle()
     finally:
-        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
     planes = rt.read(ws, (sk, m, n), np.float32)
     host = o.splitk_reduce(planes)
     got = rt.read(c, (m, n), np.float32 if out == t0g.F32 else np.uint16)
@@ -421,7 +421,7 @@ def test_split_k_grid_remap_covers_every_slice(rt, bufs, preset, tiles_m, tiles_
         rt.gemm_desc(d)
         rt.wait_idle()
     finally:
-        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
     planes = rt.read(ws, (sk, m, n), np.float32)
     assert not np.isnan(planes).any(), "a (tile, K slice) pair was not computed"
     kps = k // sk

@@ -273,10 +273,12 @@ def test_gemm_plan_selection_host_only():
 
 
 def test_split_k_mode_selects_the_reduction():
-    """By default split-K writes fp32 planes for the reduce kernel; the in-kernel mode
-    takes the _r kernel, or _dr where the grid runs the deep-ring kernel (both write
-    the output dtype and sum the planes themselves), and only where its plan
-    conditions hold; an unknown mode is refused."""
+    """By default (auto) split-K writes fp32 planes for the reduce kernel, except two K
+    slices on a deep-ring kernel, which are summed inside it (_dr, _dsr); the reduce
+    kernel mode always writes planes; the in-kernel mode takes the _r kernel, or _dr /
+    _dsr where the grid runs the deep-ring kernel (both write the output dtype and sum
+    the planes themselves), and only where its plan conditions hold; an unknown mode is
+    refused."""
     def name(m=128, n=4096, **kw):
         return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, m, n, 4096, transpose="NT",
                                                   out_dtype=t0g.BF16, **kw))
@@ -284,8 +286,16 @@ def test_split_k_mode_selects_the_reduction():
     c64 = t0g.GemmConfig.preset("gfx950_64x64_k64")
     # 32 tiles x 8 slices: one workgroup per CU, so the deep-ring kernel writes the planes
     assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
-    assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_f32_ds"     # 32 stages per split
+    # two slices on the deep ring: summed in the kernel by default
+    assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_bf16_dsr"   # 32 stages per slice
+    assert name(config=c128, split_k=2) == "t0g_gemm_128x128_k64_nt_bf16_dr"
     assert name(m=64, n=512, config=c64, split_k=4) == "t0g_gemm_64x64_k64_nt_f32_d"   # 16
+    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+    try:
+        assert name(config=c64, split_k=2) == "t0g_gemm_64x64_k64_nt_f32_ds"
+        assert name(config=c128, split_k=2) == "t0g_gemm_128x128_k64_nt_f32_d"
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
     t0g.set_split_k_mode(t0g.SPLIT_K_IN_KERNEL)
     try:
         assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_bf16_dr"
@@ -300,10 +310,10 @@ def test_split_k_mode_selects_the_reduction():
         assert name(config=c128, split_k=6) == "t0g_gemm_128x128_k64_nt_f32_d"   # not a power of two
         assert name(config=c128) == "t0g_gemm_128x128_k64_nt_bf16_d"              # no split, nothing to sum
         with pytest.raises(t0g.T0gError) as e:
-            t0g.set_split_k_mode(2)
+            t0g.set_split_k_mode(3)
         assert e.value.code == t0g.ERR_INVALID_ARG
     finally:
-        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
     assert name(config=c128, split_k=8) == "t0g_gemm_128x128_k64_nt_f32_d"
     # more workgroups than CUs: the 4-stage ring kernel, two workgroups per CU
     assert t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 4096, 4096, 4096, out_dtype=t0g.BF16,

@@ -37,7 +37,7 @@ def _log(msg):
 def rt():
     r = t0g.GpuRuntime.new(0)
     yield r
-    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+    t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
     t0g.debug_stream_k_stall(False)
     assert r.stream_k_timeouts() == 0
     r.close()
@@ -69,7 +69,7 @@ def _run(rt, da, db, m, n, k, layout, cfg, sk, out, mode, epilogue_ops=None, bia
         finally:
             rt.free(dc)
     finally:
-        t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
 
 
 CASES = [
@@ -140,7 +140,7 @@ def test_fused_epilogue_chain(rt, layout, m, n, k, cfg, sk):
             rt.gemm_desc(d)
             planes = rt.read(dc, (m, n), np.float32)
         finally:
-            t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+            t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
             rt.free(dc)
         assert np.array_equal(fused, planes)
         ref = o.epilogue_chain(o.gemm("NT", a_mk, b_nk, m, n, k), ops, bias=bias, clamp=(-0.05, 0.1))
