@@ -89,6 +89,11 @@ CASES = [
     ("NN", 192, 320, 5000, P64, 4),        # K tail on the 64x64 deep-ring kernel
     ("TN", 104, 200, 3000, P64, 8),        # ragged M and N, M-contiguous A (rows of 16-byte multiples)
     ("TT", 64, 64, 4096, P64, 16),         # a single 64x64 tile in 16 slices
+    # two slices: the second to arrive adds the first's partial (red_pair)
+    ("TN", 104, 200, 3000, P64, 2),        # ragged edges (masked stores), K tail, K split across the waves
+    ("NN", 320, 136, 3000, P128, 2),       # ragged, 128x128 deep ring
+    ("NT", 256, 512, 1024, P64, 2),        # 8 stages per slice: the 2 x 2 wave grid (_dr)
+    ("TT", 192, 256, 4096, P128, 2),       # TT on 128x128
 ]
 
 
@@ -120,7 +125,8 @@ def test_fused_equals_reduce_kernel(rt, layout, m, n, k, cfg, sk, out):
         rt.free(db)
 
 
-@pytest.mark.parametrize("layout,m,n,k,cfg,sk", [CASES[0], CASES[3], CASES[7], CASES[9], CASES[12]])
+@pytest.mark.parametrize("layout,m,n,k,cfg,sk", [CASES[0], CASES[3], CASES[7], CASES[9], CASES[10], CASES[12],
+                                                  CASES[15], CASES[16]])
 def test_fused_epilogue_chain(rt, layout, m, n, k, cfg, sk):
     """bias + SiLU + clamp applied once, after the sum (not per slice)."""
     a_mk, b_nk, a_st, b_st = _operands(layout, m, n, k, 7 + n)
