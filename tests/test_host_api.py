@@ -47,6 +47,31 @@ def test_rust_binding_declares_every_entry_point():
     assert {n: (rust_fns[n], c_fns[n]) for n in c_fns if rust_fns[n] != c_fns[n]} == {}
 
 
+def test_binding_constants_match_the_header():
+    """Every enum value and numeric #define of the header that the Python binding
+    mirrors (T0G_X as t0g.X) has the header's value."""
+    with open(os.path.join(ROOT, "include", "t0g.h")) as f:
+        body = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    vals = {}
+    for blk in re.findall(r"enum\s*\w*\s*\{(.*?)\}", body, re.S):
+        nxt = 0
+        for ent in (e.strip() for e in blk.split(",")):
+            m = re.match(r"T0G_(\w+)\s*(?:=\s*(-?\w+))?$", ent)
+            if not m:
+                continue
+            if m.group(2) is not None:
+                nxt = int(m.group(2), 0)
+            vals[m.group(1)] = nxt
+            nxt += 1
+    for name, v, sh in re.findall(r"#define T0G_(\w+)\s+\(?(0x[0-9a-fA-F]+|\d+)u?(?:\s*<<\s*(\d+))?\)?", body):
+        vals[name] = int(v, 0) << (int(sh) if sh else 0)
+    mirrored = {n: (v, getattr(t0g, n)) for n, v in vals.items() if hasattr(t0g, n)}
+    assert len(mirrored) >= 25
+    for n in ("SPLIT_K_REDUCE_KERNEL", "SPLIT_K_IN_KERNEL", "SPLIT_K_AUTO", "STREAM_K", "BF16", "TT"):
+        assert n in mirrored, n
+    assert {n: x for n, x in mirrored.items() if x[0] != x[1]} == {}
+
+
 def test_library_links_no_oracle():
     with open(t0g.LIB_PATH, "rb") as f:
         blob = f.read()
