@@ -12,7 +12,11 @@ layouts, f32 and bf16 output, ragged M/N edges, K tails, epilogue chains,
 repeated launches (the control words must be back at zero after each), the
 host-forced path in which every workgroup but a tile's last arrival gives up
 waiting, so the last arrival sums the whole tile, and a seeded sweep of random
-aligned problems (24 committed; 400 pass with T0G_FUSED_SWEEP_CASES=400)."""
+aligned problems (24 committed; 400 pass with T0G_FUSED_SWEEP_CASES=400).
+Two slices on the deep rings take the no-wait pair sum (the second slice to
+arrive adds the first's partial), the default for them: it has cases of its own,
+two handles running it at once on two streams, and replays of a captured HIP
+graph."""
 import sys
 
 import numpy as np
@@ -214,3 +218,88 @@ def test_fused_random_problem(rt, i):
     finally:
         rt.free(da)
         rt.free(db)
+
+
+def test_two_slice_sums_on_two_handles_at_once():
+    """The two-slice sum, the default for C4a's shape, keeps its arrival counters in the
+    handle's control block: two handles on two streams, eight launches each enqueued in
+    turn with no wait, give every output equal bit for bit to a single launch's."""
+    from hip_rt import Stream
+    m, n, k = 128, 4096, 4096
+    a = o.rand_bf16_lcg(m * k, 71)
+    b = o.rand_bf16_lcg(n * k, 72)
+    streams = [Stream(), Stream()]
+    hs = [t0g.GpuRuntime.new(0), t0g.GpuRuntime.new(0)]
+    try:
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
+        ops, outs = [], []
+        for h, s in zip(hs, streams):
+            h.set_stream(s.ptr)
+            da, db = h.upload(a), h.upload(b)
+            cs = [h.alloc(m * n * 4) for _ in range(8)]
+            ops.append((da, db))
+            outs.append(cs)
+        names = {t0g.gemm_kernel_name(t0g.gemm_desc(ops[0][0], ops[0][1], outs[0][0], m, n, k, config=P64,
+                                                    split_k=2))}
+        assert names == {"t0g_gemm_64x64_k64_nt_f32_dsr"}, names
+        for i in range(8):
+            for h, (da, db), cs in zip(hs, ops, outs):
+                h.gemm(da, db, cs[i], m, n, k, config=P64, split_k=2)
+        for h in hs:
+            h.wait_idle()
+        want = hs[0].read(outs[0][0], (m, n), np.float32)
+        assert o.parity(want, o.gemm("NT", a, b, m, n, k), k)[0]
+        for j, (h, cs) in enumerate(zip(hs, outs)):
+            for i, c in enumerate(cs):
+                assert np.array_equal(h.read(c, (m, n), np.float32), want), f"handle {j} launch {i}"
+        for h in hs:
+            assert h.stream_k_timeouts() == 0
+            assert not h.is_poisoned()
+            h.set_stream(None)
+    finally:
+        for h in hs:
+            h.close()
+        for s in streams:
+            s.destroy()
+
+
+def test_two_slice_sum_under_hip_graph_capture():
+    """A two-slice launch captured into a HIP graph (after an eager call set up the
+    workspace and control block; the launch itself enqueues only the kernel, and the
+    counters clear themselves) and replayed: every replay, with eager work and
+    synchronisations in between, equals the eager call bit for bit."""
+    from hip_rt import Graph, Stream
+    m, n, k = 128, 4096, 4096
+    a = o.rand_bf16_lcg(m * k, 81)
+    b = o.rand_bf16_lcg(n * k, 82)
+    h = t0g.GpuRuntime.new(0)
+    s = Stream()
+    g = None
+    try:
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
+        h.set_stream(s.ptr)
+        da, db = h.upload(a), h.upload(b)
+        c_eager, c_graph, c_other = h.alloc(m * n * 2), h.alloc(m * n * 2), h.alloc(64 * 64 * 4)
+        d_eager = t0g.gemm_desc(da, db, c_eager, m, n, k, out_dtype=t0g.BF16, config=P64, split_k=2)
+        d_graph = t0g.gemm_desc(da, db, c_graph, m, n, k, out_dtype=t0g.BF16, config=P64, split_k=2)
+        assert t0g.gemm_kernel_name(d_graph) == "t0g_gemm_64x64_k64_nt_bf16_dsr"
+        h.gemm_desc(d_eager)
+        h.wait_idle()
+        want = h.read(c_eager, (m, n), np.uint16)
+        g = Graph(s, lambda: h.gemm_desc(d_graph))
+        for rep in range(4):
+            h.memset(c_graph, 0xFF, m * n * 2)
+            g.launch(s)
+            s.synchronize()
+            assert np.array_equal(h.read(c_graph, (m, n), np.uint16), want), f"replay {rep}"
+            h.gemm(db, da, c_other, 64, 64, 4096, config=P64, split_k=2)   # eager two-slice work between
+            h.wait_idle()
+        assert h.stream_k_timeouts() == 0
+        h.set_stream(None)
+        for x in (da, db, c_eager, c_graph, c_other):
+            h.free(x)
+    finally:
+        if g is not None:
+            g.destroy()
+        h.close()
+        s.destroy()
