@@ -97,3 +97,47 @@ def test_k_split_kernels_against_the_oracle(rt, layout, m, n, k, split, mode, sf
     finally:
         rt.free(da)
         rt.free(db)
+
+
+@pytest.mark.parametrize("layout,m,n,k,split,mode,sfx", [
+    ("NT", 256, 256, 2048, 1, AUTO, "_ds"),        # the chain in the GEMM kernel's own store
+    ("TN", 104, 200, 3100, 2, AUTO, "_dsr"),       # applied once, after the two-slice sum
+    ("NN", 192, 320, 6200, 4, REDUCE, "_ds"),      # applied by the reduce kernel
+])
+def test_k_split_kernels_with_an_epilogue_chain(rt, layout, m, n, k, split, mode, sfx):
+    """bias + SiLU + scale + clamp on the K-split kernels, f32 against the oracle's chain and
+    bf16 equal to RNE of the same kernel's f32 output."""
+    _log(f"[case] K split + epilogue chain: {layout} {m}x{n}x{k} split {split} mode {mode}")
+    a_mk = _uniform_half(m * k, 17 + m + k).reshape(m, k)
+    b_nk = _uniform_half(n * k, 19 + n + k).reshape(n, k)
+    a_st = a_mk if layout[0] == "N" else np.ascontiguousarray(a_mk.T)
+    b_st = b_nk if layout[1] == "T" else np.ascontiguousarray(b_nk.T)
+    bias = ((np.arange(n, dtype=np.float32) % 5) - 2.0) * 0.25
+    ops = ["bias", "silu", "scale", "clamp"]
+    da, db, dbias = rt.upload(a_st), rt.upload(b_st), rt.upload(bias)
+    outs = {}
+    try:
+        t0g.set_split_k_mode(mode)
+        for out, esz, dt in ((t0g.F32, 4, np.float32), (t0g.BF16, 2, np.uint16)):
+            d = t0g.gemm_desc(da, db, 0, m, n, k, transpose=layout, out_dtype=out, config=P64, split_k=split,
+                              epilogue_ops=ops, bias=dbias, epi_scale=1.5, clamp=(-0.2, 0.6))
+            name = t0g.gemm_kernel_name(d)
+            assert name.startswith("t0g_gemm_64x64_k64_") and name.endswith(sfx), name
+            dc = rt.alloc(m * n * esz)
+            try:
+                rt.memset(dc, 0xFF, m * n * esz)
+                d.c = dc
+                rt.gemm_desc(d)
+                rt.wait_idle()
+                outs[out] = rt.read(dc, (m, n), dt)
+            finally:
+                rt.free(dc)
+    finally:
+        t0g.set_split_k_mode(AUTO)
+        for x in (da, db, dbias):
+            rt.free(x)
+    ref = o.epilogue_chain(o.gemm("NT", a_mk, b_nk, m, n, k), ops, bias=bias, scale=1.5, clamp=(-0.2, 0.6))
+    ok, relf, maxabs, bound = o.parity(outs[t0g.F32], ref, k)
+    _log(f"[parity] chain: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
+    assert ok
+    assert np.array_equal(outs[t0g.BF16], o.f32_to_bf16_rne(outs[t0g.F32]))
