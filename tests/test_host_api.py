@@ -449,3 +449,25 @@ def test_operand_size_limits(layout):
     with pytest.raises(t0g.T0gError) as e:    # past the bound: element-wise, which cannot take 2^31 elements
         name(m, k=kk, lda=big_ld)
     assert e.value.code == t0g.ERR_INVALID_ARG
+
+
+def test_k_split_kernels_from_24_stages_per_slice():
+    """The 64x64 deep ring splits K across its waves (_ds, or _dsr summed in the kernel) from
+    24 stages of 64 K values per slice; one stage less keeps the 2 x 2 wave grid (_d, _dr)."""
+    c64 = t0g.GemmConfig.preset("gfx950_64x64_k64")
+
+    def name(k, split, out=t0g.BF16):
+        return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, 64, 64, k, transpose="NT",
+                                                  out_dtype=out, config=c64, split_k=split))
+    assert name(23 * 64, 1) == "t0g_gemm_64x64_k64_nt_bf16_d"
+    assert name(24 * 64, 1) == "t0g_gemm_64x64_k64_nt_bf16_ds"
+    assert name(23 * 64 + 8, 1) == "t0g_gemm_64x64_k64_nt_bf16_ds"     # a 24th stage with a K tail
+    assert name(2 * 23 * 64, 2) == "t0g_gemm_64x64_k64_nt_bf16_dr"     # two slices: summed in the kernel
+    assert name(2 * 24 * 64, 2) == "t0g_gemm_64x64_k64_nt_bf16_dsr"
+    assert name(4 * 24 * 64, 4) == "t0g_gemm_64x64_k64_nt_f32_ds"      # four slices: planes + reduce
+    t0g.set_split_k_mode(t0g.SPLIT_K_REDUCE_KERNEL)
+    try:
+        assert name(2 * 24 * 64, 2) == "t0g_gemm_64x64_k64_nt_f32_ds"
+        assert name(2 * 23 * 64, 2) == "t0g_gemm_64x64_k64_nt_f32_d"
+    finally:
+        t0g.set_split_k_mode(t0g.SPLIT_K_AUTO)
