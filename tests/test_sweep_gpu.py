@@ -69,10 +69,63 @@ def _stored(logical, pad, rng):
     return np.ascontiguousarray(full)
 
 
+# Long K on the 64x64 tile: K a multiple of 8 from 1536 to 5000 and M, N up to 400, so the
+# grid stays at one workgroup per CU and slices of 24 stages or more reach the deep ring's
+# K-split kernels (_ds, and _dsr where two slices are summed in the kernel); the short-K
+# sweep above never gets there.  Padding of 13 elements still sends some cases to the
+# element-wise kernels.  16 committed; 120 pass with T0G_SWEEP_LONG_CASES=120.
+N_LONG = int(os.environ.get("T0G_SWEEP_LONG_CASES", "16"))
+
+
+def _case_long(j):
+    rng = np.random.default_rng(SEED0 + 50000 + j)
+    layout = ["NT", "NN", "TN", "TT"][j % 4]
+    # M (N) is the contiguous dimension of A (B) in TN/TT (NN/TN): a multiple of 8 there keeps
+    # the rows 16-byte aligned for the fast kernels; elsewhere it is ragged
+    m = 8 * int(rng.integers(1, 51)) if layout in ("TN", "TT") else int(rng.integers(1, 401))
+    n = 8 * int(rng.integers(1, 51)) if layout in ("NN", "TN") else int(rng.integers(1, 401))
+    k = 8 * int(rng.integers(192, 626))
+    preset = "gfx950_64x64_k64" if j % 8 != 7 else None
+    split = 0 if preset is None else int(rng.choice([1, 1, 2, 2, 4]))
+    pads = [int(rng.choice([0, 0, 0, 8, 8, 13])) if j % 4 == 2 else int(rng.choice([0, 0, 8])) for _ in range(3)]
+    out = t0g.BF16 if rng.integers(0, 2) else t0g.F32
+    chain = None
+    if j % 3 == 1:
+        names = ["bias", "scale", "relu", "silu", "gelu", "abs", "neg", "clamp"]
+        chain = [names[int(x)] for x in rng.integers(0, len(names), int(rng.integers(1, 5)))]
+    return rng, layout, m, n, k, preset, split, pads, out, chain
+
+
+def _plan_name(case):
+    _, layout, m, n, k, preset, split, pads, out, chain = case
+    a_cols = (k if layout in ("NT", "NN") else m) + pads[0]
+    b_cols = (k if layout in ("NT", "TT") else n) + pads[1]
+    kw = dict(transpose=layout, lda=a_cols, ldb=b_cols, ldc=n + pads[2], split_k=split, out_dtype=t0g.F32)
+    if preset is not None:
+        kw["config"] = t0g.GemmConfig.preset(preset)
+    if chain:
+        kw.update(epilogue_ops=chain, bias=0x40000)
+    return t0g.gemm_kernel_name(t0g.gemm_desc(0x10000, 0x20000, 0x30000, m, n, k, **kw))
+
+
+def test_long_k_sweep_reaches_the_k_split_kernels():
+    names = [_plan_name(_case_long(j)) for j in range(N_LONG)]
+    assert sum(nm.endswith(("_ds", "_dsr")) for nm in names) >= N_LONG // 3, names
+
+
+@pytest.mark.parametrize("j", range(N_LONG))
+def test_random_problem_long_k(rt, j):
+    _check(rt, 1000 + j, _case_long(j), f"long-K sweep {j}")
+
+
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_problem(rt, i):
-    rng, layout, m, n, k, preset, split, pads, out, chain = _case(i)
-    _log(f"[case] sweep {i}: {layout} {m}x{n}x{k} data={'lcg' if i % 2 == 0 else 'two-sided'} "
+    _check(rt, i, _case(i), f"sweep {i}")
+
+
+def _check(rt, i, case, tag):
+    rng, layout, m, n, k, preset, split, pads, out, chain = case
+    _log(f"[case] {tag}: {layout} {m}x{n}x{k} data={'lcg' if i % 2 == 0 else 'two-sided'} "
          f"preset={preset} split={split} pads={pads} "
          f"out={'bf16' if out == t0g.BF16 else 'f32'} chain={chain}")
     if i % 2 == 0:
@@ -117,7 +170,7 @@ def test_random_problem(rt, i):
         if chain:
             ref = o.epilogue_chain(ref, chain, bias=bias, scale=kw["epi_scale"], clamp=kw["clamp"])
         ok, relf, maxabs, bound = o.parity(c, ref, k)
-        _log(f"[parity] sweep {i}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
+        _log(f"[parity] {tag}: relF={relf:.3e} max|d|={maxabs:.3e} (bound {bound:.3e})")
         assert ok, f"relF={relf:.3e} max|d|={maxabs:.3e} bound={bound:.3e}"
         if out == t0g.BF16:
             rt.memset(dc2, 0xFF, m * ldc * 2)
